@@ -1,0 +1,197 @@
+/*
+ * origami_layout.h -- C ABI of the MI355X (gfx950) Origami KV codec-layout
+ * library, liborigami_layout.so.
+ *
+ * The library replaces the layout/bitpack part of Origami's CUDA extension
+ * (csrc/origami/bitpack_layout_cuda.cpp + bitpack_layout_cuda.cu, loaded as
+ * `origami_bitpack_cuda_v6` by lossless/native_gpu.py:35-49).  Every entry
+ * point takes plain pointers and sizes: device buffers are raw device
+ * addresses, metadata arrays are host memory, and the stream is a hipStream_t.
+ * No torch types cross this boundary.
+ *
+ * Conventions (mirroring the reference's torch extension):
+ *  - Return value: ORIGAMI_OK (0) or an error code; origami_last_error()
+ *    returns the message of the last failure on the calling thread.  The
+ *    reference raised RuntimeError from TORCH_CHECK with these messages.
+ *  - Chunk metadata follows the reference wire format: chunk_specs is
+ *    [num_chunks, 6] int64 rows (head_start, head_end, channel_start,
+ *    channel_end, token_start, token_end); chunk_offsets is [num_chunks + 1]
+ *    byte offsets into the flat stream; bits_per_chunk is [num_chunks] with
+ *    values 1..8.  Symbols are LSB-first, head-major, then channel, token
+ *    fastest (bitpack_layout_cuda.cu:70-128).
+ *  - source_shape is the rank-3/4 symbol tensor shape and axis_positions is
+ *    [token_axis, head_axis, head_dim_axis, layer_axis or -1]
+ *    (lossless/native_cpu.py:102-130).
+ *  - Metadata is read on the host only: unlike the reference
+ *    (bitpack_layout_cuda.cpp:156, 350-351) no call copies device memory
+ *    back to the host.  Device copies of the metadata the kernels need are
+ *    made once per distinct layout and cached inside the library.
+ *  - All device work is enqueued on `stream` and is asynchronous.  Inputs
+ *    must stay alive until that work completes.
+ *  - kv_cache layout codes: ORIGAMI_CACHE_KV_FIRST is [2, num_blocks,
+ *    block_size, num_heads, head_dim]; ORIGAMI_CACHE_BLOCKS_FIRST is
+ *    [num_blocks, 2, block_size, num_heads, head_dim]
+ *    (bitpack_layout_cuda.cpp:526-552).  head_bytes = head_dim * element size.
+ *  - Block ids are int64 device arrays.  Ids outside [0, num_blocks) are
+ *    skipped by the kernels, as the reference's fused kernels do
+ *    (bitpack_layout_cuda.cu:389-392); callers validate them beforehand.
+ */
+#ifndef ORIGAMI_LAYOUT_H_
+#define ORIGAMI_LAYOUT_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* origami_stream_t; /* == hipStream_t */
+
+#define ORIGAMI_OK 0
+#define ORIGAMI_ERR_INVALID 1     /* invalid argument (reference: TORCH_CHECK) */
+#define ORIGAMI_ERR_UNSUPPORTED 2 /* layout not served by the requested fused path */
+#define ORIGAMI_ERR_HIP 3         /* HIP runtime failure */
+
+#define ORIGAMI_CACHE_KV_FIRST 0
+#define ORIGAMI_CACHE_BLOCKS_FIRST 1
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* origami_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int origami_abi_version(void);
+
+/*
+ * Host-only validation of a canonical chunk layout.  Replaces the checks of
+ * read_source_layout / read_chunk_specs / check_bits /
+ * packed_bytes_for_symbols and the byte-size loop of
+ * unpack_canonical_storage_chunks_cuda (bitpack_layout_cuda.cpp:43-185,
+ * 326-362), plus a bound the reference lacks: chunk_offsets must be
+ * non-decreasing and end within flat_bytes.
+ */
+int origami_validate_chunks(const int64_t* chunk_offsets,
+                            const int64_t* bits_per_chunk,
+                            const int64_t* chunk_specs, int64_t num_chunks,
+                            const int64_t* source_shape, int64_t rank,
+                            const int64_t* axis_positions, int64_t token_count,
+                            int64_t num_heads, int64_t head_dim,
+                            int64_t flat_bytes);
+
+/*
+ * Host-only plane plan (new; no reference counterpart, used by tests and
+ * diagnostics).  A plane is one (head, channel) pair; its symbols are the
+ * token run of that pair inside its chunk.  Writes table[h * head_dim + c] =
+ * bit offset of token 0 of plane (h, c) in the flat stream, or -1 when no
+ * chunk covers it, and info[0..3] = {regular, uniform bits or 0,
+ * planes 16-byte aligned, planes byte aligned}.  "regular" means every chunk
+ * spans the whole token axis and no plane is covered twice, which is what
+ * the fused row kernels need.  table_len must be num_heads * head_dim.
+ */
+int origami_plan_planes(const int64_t* chunk_offsets,
+                        const int64_t* bits_per_chunk,
+                        const int64_t* chunk_specs, int64_t num_chunks,
+                        int64_t token_count, int64_t num_heads,
+                        int64_t head_dim, int64_t* table, int64_t table_len,
+                        int64_t* info);
+
+/*
+ * Unpack a flat stream of canonical chunks into a zero-initialised uint8
+ * symbol tensor of prod(source_shape) bytes in the source layout.
+ * Replaces unpack_canonical_storage_chunks_cuda (bitpack_layout_cuda.cpp:
+ * 316-400) and origami_unpack_canonical_storage_chunks_launch
+ * (bitpack_layout_cuda.cu:190-243).  Bytes no chunk covers are 0.
+ */
+int origami_unpack_canonical_storage_chunks(
+    const uint8_t* flat_chunks, int64_t flat_bytes,
+    const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
+    const int64_t* chunk_specs, int64_t num_chunks,
+    const int64_t* source_shape, int64_t rank, const int64_t* axis_positions,
+    int64_t token_count, int64_t num_heads, int64_t head_dim,
+    uint8_t* output, int64_t output_bytes, origami_stream_t stream);
+
+/*
+ * Pack a uint8 symbol tensor (source layout) into the flat canonical stream:
+ * the inverse of origami_unpack_canonical_storage_chunks, with zero pad bits
+ * after each chunk's last symbol.  Replaces the stub
+ * native_cpu.pack_canonical_storage_chunks (lossless/native_cpu.py:144-151),
+ * which raises in the reference.  flat_bytes must be >= chunk_offsets[N].
+ */
+int origami_pack_canonical_storage_chunks(
+    const uint8_t* symbols, int64_t symbol_bytes,
+    const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
+    const int64_t* chunk_specs, int64_t num_chunks,
+    const int64_t* source_shape, int64_t rank, const int64_t* axis_positions,
+    int64_t token_count, int64_t num_heads, int64_t head_dim,
+    uint8_t* flat_chunks, int64_t flat_bytes, origami_stream_t stream);
+
+/*
+ * Fused restore: unpack one layer's canonical stream and scatter it into the
+ * paged KV cache through the block table, in one pass.  The layer's symbols
+ * are the bytes of its token-major K/V, viewed as [2 * tokens, num_heads,
+ * head_bytes] (K tokens, then V tokens; chunk_specs index that tensor).
+ * Destination tokens [0, block_count * block_size) of K and V are written;
+ * tokens >= `tokens` are written as zero (the tail padding of
+ * benchmark_utils.py:378-392).  Replaces the chain
+ * unpack_canonical_storage_chunks_cuda -> RawBytesTensorAdapter.dequantize
+ * -> copy_kv_to_hbm (worker.py:1087-1248, raw_tensor.py:125-157,
+ * benchmark_utils.py:350-444); the destination index is that of
+ * bitpack_layout_cuda.cu:408-420.  Returns ORIGAMI_ERR_UNSUPPORTED when the
+ * chunk plan is not regular or head_bytes is not a multiple of 16; the caller
+ * then unpacks and scatters in two steps.
+ */
+int origami_unpack_canonical_to_kv_cache(
+    const uint8_t* flat_chunks, int64_t flat_bytes,
+    const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
+    const int64_t* chunk_specs, int64_t num_chunks, int64_t tokens,
+    void* kv_cache, int64_t cache_layout, int64_t num_blocks,
+    int64_t block_size, int64_t num_heads, int64_t head_bytes,
+    const int64_t* block_ids, int64_t block_count, origami_stream_t stream);
+
+/*
+ * Fused save: gather a layer's K/V through the block table from the paged
+ * cache and pack it into the canonical stream, in one pass; the inverse of
+ * origami_unpack_canonical_to_kv_cache.  Replaces _select_blocks +
+ * RawBytesTensorAdapter.quantize + the packer of _pack_quantized_symbols
+ * (worker.py:1881-2040, raw_tensor.py:100-123).  Tokens are [0, tokens) of
+ * the blocks listed.  Returns ORIGAMI_ERR_UNSUPPORTED unless the plan is
+ * regular, every plane starts on a byte boundary and tokens * bits is a
+ * multiple of 8.
+ */
+int origami_pack_canonical_from_kv_cache(
+    const void* kv_cache, int64_t cache_layout, int64_t num_blocks,
+    int64_t block_size, int64_t num_heads, int64_t head_bytes,
+    const int64_t* block_ids, int64_t block_count, int64_t tokens,
+    const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
+    const int64_t* chunk_specs, int64_t num_chunks, uint8_t* flat_chunks,
+    int64_t flat_bytes, origami_stream_t stream);
+
+/*
+ * Paged scatter of a token-major K/V tensor (bytes of [2, tokens, num_heads,
+ * head_bytes]) into the cache, zero-padding to whole blocks.  Replaces
+ * copy_kv_to_hbm / _assign_blocks / _normalize_kv_value
+ * (benchmark_utils.py:350-444) for device-resident values.
+ */
+int origami_scatter_kv_blocks(const uint8_t* value, int64_t tokens,
+                              void* kv_cache, int64_t cache_layout,
+                              int64_t num_blocks, int64_t block_size,
+                              int64_t num_heads, int64_t head_bytes,
+                              const int64_t* block_ids, int64_t block_count,
+                              origami_stream_t stream);
+
+/*
+ * Block gather from the cache into a token-major K/V tensor (bytes of
+ * [2, block_count * block_size, num_heads, head_bytes]).  Replaces
+ * _select_blocks (worker.py:1881-1897) + the byte view of
+ * RawBytesTensorAdapter.quantize (raw_tensor.py:100-123).
+ */
+int origami_gather_kv_blocks(const void* kv_cache, int64_t cache_layout,
+                             int64_t num_blocks, int64_t block_size,
+                             int64_t num_heads, int64_t head_bytes,
+                             const int64_t* block_ids, int64_t block_count,
+                             uint8_t* value, origami_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ORIGAMI_LAYOUT_H_ */

@@ -1,0 +1,1179 @@
+// origami_layout.hip -- MI355X (gfx950) kernels and C ABI for Origami's
+// canonical KV codec layout: pack, unpack, fused unpack+scatter into the paged
+// KV cache, fused gather+pack from it, and paged block copies.
+//
+// Canonical format (the reference decoder, csrc/origami/bitpack_layout_cuda.cu
+// :70-128): a layer's uint8 symbol tensor is cut into chunks
+// [head range x channel range x token range]; inside a chunk symbols run
+// head-major, then channel, token fastest, packed LSB-first at b bits
+// (b = 8 is the identity).  A "plane" is one (head, channel) pair: its token
+// run is contiguous in the stream.
+//
+// Kernel design (wave64, 16-byte lanes):
+//  * rows kernels (the hot path).  A lane owns a 16-channel x 16-token byte
+//    tile.  It reads the 16 planes' 16-token runs (one 16-byte load each when
+//    b = 8 and aligned), transposes the 16x16 bytes in registers with
+//    v_perm_b32, and writes 16 destination rows of 16 bytes.  Eight lanes
+//    share a channel group and cover 128 consecutive tokens (a full 128-byte
+//    line of a plane per load instruction); eight lanes share a token and
+//    cover 128 consecutive channels (a full 128-byte line of a destination
+//    row per store instruction).  No LDS is needed for the data; LDS holds
+//    only the 128 plane descriptors a workgroup shares.
+//  * generic kernels: one thread per symbol / per output byte, for layouts the
+//    rows kernels do not serve (irregular chunk plans, channel-major layouts).
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include <algorithm>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "origami_layout.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Errors
+// ---------------------------------------------------------------------------
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    return fail(ORIGAMI_ERR_HIP, std::string(what) + ": " + hipGetErrorString(err));
+  }
+  return ORIGAMI_OK;
+}
+
+#define ORIGAMI_REQUIRE(cond, msg)              \
+  do {                                          \
+    if (!(cond)) return fail(ORIGAMI_ERR_INVALID, msg); \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Host-side layout helpers
+// ---------------------------------------------------------------------------
+
+struct Strides {
+  int64_t token, head, channel;
+};
+
+int64_t spec_symbols(const int64_t* s) {
+  return (s[1] - s[0]) * (s[3] - s[2]) * (s[5] - s[4]);
+}
+
+// Validation the reference performs in read_source_layout / read_chunk_specs
+// / check_bits / the byte-size loop (bitpack_layout_cuda.cpp:43-185, 326-362),
+// with the same messages, plus stream bounds the reference does not check.
+int validate_layout(const int64_t* offsets, const int64_t* bits,
+                    const int64_t* specs, int64_t n, const int64_t* shape,
+                    int64_t rank, const int64_t* axes, int64_t token_count,
+                    int64_t num_heads, int64_t head_dim, int64_t flat_bytes,
+                    Strides* strides) {
+  ORIGAMI_REQUIRE(n >= 0, "chunk count must be non-negative");
+  ORIGAMI_REQUIRE(token_count > 0 && num_heads > 0 && head_dim > 0,
+                  "canonical symbol shape must be positive");
+  ORIGAMI_REQUIRE(rank == 3 || rank == 4,
+                  "Origami source layout supports rank 3 or rank 4");
+  int64_t stride[4] = {1, 1, 1, 1};
+  for (int64_t a = 0; a < rank; ++a)
+    ORIGAMI_REQUIRE(shape[a] > 0, "source_shape dimensions must be positive");
+  for (int64_t a = rank - 2; a >= 0; --a) stride[a] = stride[a + 1] * shape[a + 1];
+  ORIGAMI_REQUIRE(axes[0] >= 0 && axes[0] < rank,
+                  "token axis must be present in source layout");
+  ORIGAMI_REQUIRE(axes[1] >= 0 && axes[1] < rank,
+                  "head axis must be present in source layout");
+  ORIGAMI_REQUIRE(axes[2] >= 0 && axes[2] < rank,
+                  "head_dim axis must be present in source layout");
+  ORIGAMI_REQUIRE(axes[3] == -1 || (axes[3] >= 0 && axes[3] < rank),
+                  "layer axis must be -1 or present in source layout");
+  ORIGAMI_REQUIRE(shape[axes[0]] == token_count,
+                  "source token axis size must match token_count");
+  ORIGAMI_REQUIRE(shape[axes[1]] == num_heads,
+                  "source head axis size must match num_heads");
+  ORIGAMI_REQUIRE(shape[axes[2]] == head_dim,
+                  "source head_dim axis size must match head_dim");
+  if (axes[3] != -1)
+    ORIGAMI_REQUIRE(shape[axes[3]] == 1,
+                    "per-layer Origami native layout requires layer axis size 1");
+  {
+    // the four axes must be distinct
+    bool seen[4] = {false, false, false, false};
+    for (int i = 0; i < 4; ++i) {
+      if (axes[i] < 0) continue;
+      ORIGAMI_REQUIRE(!seen[axes[i]], "source layout axes must be unique");
+      seen[axes[i]] = true;
+    }
+  }
+  if (n > 0) ORIGAMI_REQUIRE(offsets[0] >= 0, "chunk_offsets must be non-negative");
+  for (int64_t k = 0; k < n; ++k) {
+    const int64_t* s = specs + 6 * k;
+    ORIGAMI_REQUIRE(0 <= s[0] && s[0] < s[1] && s[1] <= num_heads,
+                    "invalid head range in Origami chunk spec");
+    ORIGAMI_REQUIRE(0 <= s[2] && s[2] < s[3] && s[3] <= head_dim,
+                    "invalid channel range in Origami chunk spec");
+    ORIGAMI_REQUIRE(0 <= s[4] && s[4] < s[5] && s[5] <= token_count,
+                    "invalid token range in Origami chunk spec");
+    ORIGAMI_REQUIRE(bits[k] >= 1 && bits[k] <= 8,
+                    "Origami CUDA bitpack supports only 1..8 bit symbols");
+    ORIGAMI_REQUIRE(offsets[k + 1] - offsets[k] == (spec_symbols(s) * bits[k] + 7) / 8,
+                    "Origami CUDA packed chunk byte size mismatch");
+  }
+  if (n > 0)
+    ORIGAMI_REQUIRE(offsets[n] <= flat_bytes,
+                    "chunk_offsets exceed the flat stream length");
+  if (strides) {
+    strides->token = stride[axes[0]];
+    strides->head = stride[axes[1]];
+    strides->channel = stride[axes[2]];
+  }
+  return ORIGAMI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Plans: host plane table + device copies of the metadata, cached per layout
+// ---------------------------------------------------------------------------
+
+constexpr int64_t kMaxPlaneTable = int64_t(1) << 20;  // planes per plan (8 MiB)
+constexpr size_t kMaxPlans = 256;
+
+struct PlanInfo {
+  bool regular = false;      // full token span per chunk, no plane twice
+  int bits = 0;              // uniform symbol width, 0 when mixed
+  bool aligned16 = false;    // every plane starts on a 16-byte boundary
+  bool byte_aligned = false; // every plane starts on a byte boundary
+};
+
+// Builds the plane table: table[h*C + c] = bit offset of token 0 of plane
+// (h, c), or -1.  Local plane order inside a chunk is head-major then channel
+// (bitpack_layout_cuda.cu:110-124), so plane (h, c) of chunk k starts at
+// symbol ((h - hs) * Cc + (c - cs)) * Tc.
+PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
+                           const int64_t* specs, int64_t n, int64_t T,
+                           int64_t H, int64_t C, int64_t* table) {
+  PlanInfo info;
+  std::fill(table, table + H * C, int64_t(-1));
+  info.regular = n > 0;
+  info.bits = n > 0 ? static_cast<int>(bits[0]) : 0;
+  info.aligned16 = true;
+  info.byte_aligned = true;
+  for (int64_t k = 0; k < n; ++k) {
+    const int64_t* s = specs + 6 * k;
+    if (bits[k] != info.bits) info.bits = 0;
+    if (s[4] != 0 || s[5] != T) {
+      info.regular = false;
+      continue;
+    }
+    const int64_t Cc = s[3] - s[2];
+    for (int64_t h = s[0]; h < s[1]; ++h) {
+      for (int64_t c = s[2]; c < s[3]; ++c) {
+        const int64_t local = (h - s[0]) * Cc + (c - s[2]);
+        const int64_t bit_off = offsets[k] * 8 + local * T * bits[k];
+        int64_t& slot = table[h * C + c];
+        if (slot != -1) info.regular = false;
+        slot = bit_off;
+        if (bit_off % 128 != 0) info.aligned16 = false;
+        if (bit_off % 8 != 0) info.byte_aligned = false;
+      }
+    }
+  }
+  if (info.bits != 8) info.aligned16 = false;
+  if (!info.regular) {
+    info.aligned16 = false;
+    info.byte_aligned = false;
+  }
+  return info;
+}
+
+struct Plan {
+  std::vector<int64_t> key;
+  int device = -1;
+  int64_t n = 0, T = 0, H = 0, C = 0, max_symbols = 0;
+  PlanInfo info;
+  bool has_table = false;
+  void* dev = nullptr;  // one allocation: offsets | bits | specs | table
+  const int64_t* d_offsets = nullptr;
+  const int64_t* d_bits = nullptr;
+  const int64_t* d_specs = nullptr;
+  const int64_t* d_table = nullptr;
+};
+
+std::mutex g_plan_mutex;
+std::unordered_map<uint64_t, std::vector<std::unique_ptr<Plan>>> g_plans;
+size_t g_plan_count = 0;
+
+uint64_t hash_words(const std::vector<int64_t>& w) {
+  uint64_t h = 1469598103934665603ull;
+  for (int64_t v : w) {
+    h ^= static_cast<uint64_t>(v);
+    h *= 1099511628211ull;
+    h ^= h >> 29;
+  }
+  return h;
+}
+
+void drop_all_plans() {
+  // Kernels may still read cached metadata: wait for the device first.
+  (void)hipDeviceSynchronize();
+  for (auto& kv : g_plans)
+    for (auto& p : kv.second)
+      if (p->dev) (void)hipFree(p->dev);
+  g_plans.clear();
+  g_plan_count = 0;
+}
+
+// Returns the cached plan for this metadata on the current device, creating
+// it (one hipMalloc + one synchronous upload) on first use.
+int get_plan(const int64_t* offsets, const int64_t* bits, const int64_t* specs,
+             int64_t n, int64_t T, int64_t H, int64_t C, bool want_table,
+             const Plan** out) {
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess)
+    return fail(ORIGAMI_ERR_HIP, "hipGetDevice failed");
+  std::vector<int64_t> key;
+  key.reserve(static_cast<size_t>(8 * n + 8));
+  key.push_back(n);
+  key.push_back(T);
+  key.push_back(H);
+  key.push_back(C);
+  key.push_back(device);
+  key.push_back(want_table ? 1 : 0);
+  key.insert(key.end(), offsets, offsets + n + 1);
+  key.insert(key.end(), bits, bits + n);
+  key.insert(key.end(), specs, specs + 6 * n);
+  const uint64_t h = hash_words(key);
+
+  std::lock_guard<std::mutex> lock(g_plan_mutex);
+  auto it = g_plans.find(h);
+  if (it != g_plans.end()) {
+    for (auto& p : it->second) {
+      if (p->key == key) {
+        *out = p.get();
+        return ORIGAMI_OK;
+      }
+    }
+  }
+  if (g_plan_count >= kMaxPlans) drop_all_plans();
+
+  auto plan = std::make_unique<Plan>();
+  plan->key = key;
+  plan->device = device;
+  plan->n = n;
+  plan->T = T;
+  plan->H = H;
+  plan->C = C;
+  for (int64_t k = 0; k < n; ++k)
+    plan->max_symbols = std::max(plan->max_symbols, spec_symbols(specs + 6 * k));
+  std::vector<int64_t> table;
+  if (want_table && H * C <= kMaxPlaneTable) {
+    table.resize(static_cast<size_t>(H * C));
+    plan->info = build_plane_table(offsets, bits, specs, n, T, H, C, table.data());
+    plan->has_table = true;
+  }
+  const size_t words = static_cast<size_t>((n + 1) + n + 6 * n) + table.size();
+  std::vector<int64_t> host(words);
+  size_t pos = 0;
+  std::memcpy(host.data() + pos, offsets, sizeof(int64_t) * (n + 1));
+  pos += n + 1;
+  std::memcpy(host.data() + pos, bits, sizeof(int64_t) * n);
+  pos += n;
+  std::memcpy(host.data() + pos, specs, sizeof(int64_t) * 6 * n);
+  pos += 6 * n;
+  if (!table.empty()) std::memcpy(host.data() + pos, table.data(), sizeof(int64_t) * table.size());
+  if (hipMalloc(&plan->dev, words * sizeof(int64_t)) != hipSuccess)
+    return fail(ORIGAMI_ERR_HIP, "hipMalloc of the layout plan failed");
+  if (hipMemcpy(plan->dev, host.data(), words * sizeof(int64_t), hipMemcpyHostToDevice) !=
+      hipSuccess) {
+    (void)hipFree(plan->dev);
+    return fail(ORIGAMI_ERR_HIP, "upload of the layout plan failed");
+  }
+  const int64_t* base = static_cast<const int64_t*>(plan->dev);
+  plan->d_offsets = base;
+  plan->d_bits = base + (n + 1);
+  plan->d_specs = base + (n + 1) + n;
+  plan->d_table = table.empty() ? nullptr : base + (n + 1) + n + 6 * n;
+  *out = plan.get();
+  g_plans[h].push_back(std::move(plan));
+  ++g_plan_count;
+  return ORIGAMI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;  // wave tiles per workgroup (along tokens)
+constexpr int kSegTokens = 16;         // tokens per lane
+constexpr int kLaneSegs = 8;           // lanes along tokens in a wave tile
+constexpr int kLaneGroups = 8;         // lanes along 16-channel groups
+constexpr int kTilePlanes = kLaneGroups * 16;  // planes per wave tile (128)
+constexpr int kTileTokens = kWaves * kLaneSegs * kSegTokens;  // per workgroup (512)
+
+struct RowsParams {
+  uint8_t* stream;           // 4-byte aligned base of the flat stream
+  int64_t stream_bytes;      // bytes addressable from `stream`
+  int64_t bit_bias;          // (caller's stream pointer - stream) * 8
+  const int64_t* planes;     // [H*C] plane bit offsets (caller pointer based)
+  uint8_t* rows;             // row base: destination (unpack) or source (pack)
+  const int64_t* block_ids;  // nullptr: identity rows
+  int64_t num_blocks;        // valid block ids are [0, num_blocks)
+  int64_t T;                 // valid tokens per half
+  int64_t row_tokens;        // destination tokens per half
+  int64_t C;                 // channels (bytes) per head
+  int64_t row_pitch;         // bytes between consecutive rows
+  int64_t head_pitch;        // bytes between heads inside a row
+  int64_t bs;                // rows per block
+  int64_t blk_stride;        // rows per block-id step
+  int64_t half_stride;       // rows per half step
+  int32_t H;
+  int32_t nq;                // C / 16
+  int32_t nqg;               // ceil(nq / 8)
+  int32_t nsg_wg;            // workgroups along tokens
+};
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// 4x4 byte transpose: o_r byte i = a_i byte r.
+__device__ __forceinline__ void transpose4x4(uint32_t a0, uint32_t a1, uint32_t a2,
+                                             uint32_t a3, uint32_t& o0, uint32_t& o1,
+                                             uint32_t& o2, uint32_t& o3) {
+  const uint32_t t0 = perm(a1, a0, 0x05010400u);  // a0.b0 a1.b0 a0.b1 a1.b1
+  const uint32_t t1 = perm(a1, a0, 0x07030602u);  // a0.b2 a1.b2 a0.b3 a1.b3
+  const uint32_t t2 = perm(a3, a2, 0x05010400u);
+  const uint32_t t3 = perm(a3, a2, 0x07030602u);
+  o0 = perm(t2, t0, 0x05040100u);
+  o1 = perm(t2, t0, 0x07060302u);
+  o2 = perm(t3, t1, 0x05040100u);
+  o3 = perm(t3, t1, 0x07060302u);
+}
+
+// 16x16 byte transpose: out[j] byte i = in[i] byte j, with rows stored as
+// 4 dwords (byte i of row r lives in dword i/4, byte i%4).
+__device__ __forceinline__ void transpose16(const uint32_t (&in)[16][4],
+                                            uint32_t (&out)[16][4]) {
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      transpose4x4(in[4 * n][m], in[4 * n + 1][m], in[4 * n + 2][m], in[4 * n + 3][m],
+                   out[4 * m][n], out[4 * m + 1][n], out[4 * m + 2][n], out[4 * m + 3][n]);
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t load_dword_guarded(const uint8_t* base, int64_t byte,
+                                                       int64_t nbytes) {
+  if (byte + 4 <= nbytes) return *reinterpret_cast<const uint32_t*>(base + byte);
+  uint32_t w = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    if (byte + b < nbytes) w |= static_cast<uint32_t>(base[byte + b]) << (8 * b);
+  return w;
+}
+
+// Spreads 16 b-bit symbols packed LSB-first in u[] into 16 bytes.
+template <int BITS>
+__device__ __forceinline__ void expand16(const uint32_t* u, uint32_t (&out)[4]) {
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = u[i];
+  } else {
+    constexpr uint32_t mask = (1u << BITS) - 1u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int bp = j * BITS;
+      const int dw = bp >> 5, off = bp & 31;
+      uint32_t s = u[dw] >> off;
+      if (off + BITS > 32) s |= u[dw + 1] << (32 - off);
+      out[j >> 2] |= (s & mask) << (8 * (j & 3));
+    }
+  }
+}
+
+// Packs 16 bytes (symbols, masked to b bits) LSB-first into u[].
+template <int BITS>
+__device__ __forceinline__ void compress16(const uint32_t (&in)[4], uint32_t* u) {
+  constexpr int NU = (16 * BITS + 31) / 32;
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = in[i];
+  } else {
+    constexpr uint32_t mask = (1u << BITS) - 1u;
+#pragma unroll
+    for (int i = 0; i < NU; ++i) u[i] = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t s = (in[j >> 2] >> (8 * (j & 3))) & mask;
+      const int bp = j * BITS;
+      const int dw = bp >> 5, off = bp & 31;
+      u[dw] |= s << off;
+      if (off + BITS > 32) u[dw + 1] |= s >> (32 - off);
+    }
+  }
+}
+
+// Loads the 16 symbols starting at stream bit P into 16 bytes.
+template <int BITS, bool ALIGNED>
+__device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
+                                               uint32_t (&out)[4]) {
+  if constexpr (ALIGNED) {
+    static_assert(BITS == 8, "aligned loads are for 8-bit symbols");
+    const uint4 x = *reinterpret_cast<const uint4*>(p.stream + (P >> 3));
+    out[0] = x.x;
+    out[1] = x.y;
+    out[2] = x.z;
+    out[3] = x.w;
+  } else {
+    constexpr int NU = (16 * BITS + 31) / 32;
+    constexpr int NW = NU + 1;
+    const int64_t d0 = P >> 5;
+    const uint32_t sh = static_cast<uint32_t>(P & 31);
+    uint32_t w[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) w[i] = load_dword_guarded(p.stream, (d0 + i) * 4, p.stream_bytes);
+    uint32_t u[NU > 4 ? NU : 4];
+#pragma unroll
+    for (int i = 0; i < NU; ++i) u[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sh);
+    expand16<BITS>(u, out);
+  }
+}
+
+// Writes nbytes of u[] (little-endian) to dst, a byte address in the stream.
+template <bool ALIGNED>
+__device__ __forceinline__ void store_stream(uint8_t* dst, const uint32_t* u, int nbytes) {
+  if constexpr (ALIGNED) {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(u[0], u[1], u[2], u[3]);
+  } else {
+    int b = 0;
+    if ((reinterpret_cast<uintptr_t>(dst) & 3) == 0) {
+      for (; b + 4 <= nbytes; b += 4) *reinterpret_cast<uint32_t*>(dst + b) = u[b >> 2];
+    }
+    for (; b < nbytes; ++b) dst[b] = static_cast<uint8_t>(u[b >> 2] >> (8 * (b & 3)));
+  }
+}
+
+struct TileCoord {
+  int h, half, ql, q;
+  int64_t t0;
+};
+
+__device__ __forceinline__ TileCoord tile_coord(const RowsParams& p) {
+  int64_t bid = blockIdx.x;
+  const int sgw = static_cast<int>(bid % p.nsg_wg);
+  bid /= p.nsg_wg;
+  const int qg = static_cast<int>(bid % p.nqg);
+  bid /= p.nqg;
+  TileCoord tc;
+  tc.h = static_cast<int>(bid % p.H);
+  tc.half = static_cast<int>(bid / p.H);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  tc.ql = lane >> 3;
+  tc.q = qg * kLaneGroups + tc.ql;
+  tc.t0 = (static_cast<int64_t>(sgw * kWaves + wave) * kLaneSegs + (lane & 7)) * kSegTokens;
+  return tc;
+}
+
+__device__ __forceinline__ void load_descriptors(const RowsParams& p, int64_t* desc) {
+  const int qg = static_cast<int>((blockIdx.x / p.nsg_wg) % p.nqg);
+  const int h = static_cast<int>((blockIdx.x / p.nsg_wg / p.nqg) % p.H);
+  if (threadIdx.x < kTilePlanes) {
+    const int64_t c = static_cast<int64_t>(qg) * kTilePlanes + threadIdx.x;
+    desc[threadIdx.x] = c < p.C ? p.planes[static_cast<int64_t>(h) * p.C + c] : -1;
+  }
+  __syncthreads();
+}
+
+// Row cursor over the 16 tokens of a lane: follows the block table.
+struct RowCursor {
+  int64_t blk, off, pid;
+};
+
+__device__ __forceinline__ void cursor_init(const RowsParams& p, int64_t t0, RowCursor& rc) {
+  if (p.block_ids) {
+    rc.blk = t0 / p.bs;
+    rc.off = t0 - rc.blk * p.bs;
+    rc.pid = p.block_ids[rc.blk];
+  } else {
+    rc.blk = 0;
+    rc.off = t0;
+    rc.pid = 0;
+  }
+}
+
+// Advances to the next token (call for j > 0 only, with that token < row_tokens).
+__device__ __forceinline__ void cursor_next(const RowsParams& p, RowCursor& rc) {
+  ++rc.off;
+  if (p.block_ids && rc.off == p.bs) {
+    rc.off = 0;
+    ++rc.blk;
+    rc.pid = p.block_ids[rc.blk];
+  }
+}
+
+// Row index of the cursor's token, or -1 for a block id outside the cache.
+__device__ __forceinline__ int64_t cursor_row(const RowsParams& p, int half, const RowCursor& rc) {
+  if (!p.block_ids) return half * p.half_stride + rc.off;
+  if (rc.pid < 0 || rc.pid >= p.num_blocks) return -1;
+  return rc.pid * p.blk_stride + half * p.half_stride + rc.off;
+}
+
+// ---------------------------------------------------------------------------
+// Rows kernels
+// ---------------------------------------------------------------------------
+
+template <int BITS, bool ALIGNED>
+__global__ __launch_bounds__(kThreads) void rows_unpack_kernel(RowsParams p) {
+  __shared__ int64_t desc[kTilePlanes];
+  load_descriptors(p, desc);
+  const TileCoord tc = tile_coord(p);
+  if (tc.q >= p.nq || tc.t0 >= p.row_tokens) return;
+  const int64_t nv = p.T - tc.t0;  // tokens of this segment that hold symbols
+  const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
+
+  uint32_t v[16][4];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t d = desc[tc.ql * 16 + k];
+    if (d < 0 || nv <= 0) {
+      v[k][0] = v[k][1] = v[k][2] = v[k][3] = 0;
+    } else {
+      load_symbols16<BITS, ALIGNED>(p, d + p.bit_bias + sym0 * BITS, v[k]);
+    }
+  }
+  if (!ALIGNED && nv < 16) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int64_t keep = nv - 4 * m;
+      const uint32_t mask = keep >= 4 ? 0xffffffffu
+                            : keep <= 0 ? 0u
+                                        : ((1u << (8 * keep)) - 1u);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k][m] &= mask;
+    }
+  }
+  uint32_t o[16][4];
+  transpose16(v, o);
+
+  RowCursor rc;
+  cursor_init(p, tc.t0, rc);
+  uint8_t* col = p.rows + static_cast<int64_t>(tc.h) * p.head_pitch + tc.q * 16;
+  const int64_t nrows = p.row_tokens - tc.t0;  // > 0 here
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (j < nrows) {
+      if (j > 0) cursor_next(p, rc);
+      const int64_t row = cursor_row(p, tc.half, rc);
+      if (row >= 0)
+        *reinterpret_cast<uint4*>(col + row * p.row_pitch) =
+            make_uint4(o[j][0], o[j][1], o[j][2], o[j][3]);
+    }
+  }
+}
+
+template <int BITS, bool ALIGNED>
+__global__ __launch_bounds__(kThreads) void rows_pack_kernel(RowsParams p) {
+  __shared__ int64_t desc[kTilePlanes];
+  load_descriptors(p, desc);
+  const TileCoord tc = tile_coord(p);
+  if (tc.q >= p.nq || tc.t0 >= p.T) return;
+  const int nv = static_cast<int>(p.T - tc.t0 < 16 ? p.T - tc.t0 : 16);
+
+  uint32_t r[16][4];
+  RowCursor rc;
+  cursor_init(p, tc.t0, rc);
+  const uint8_t* col = p.rows + static_cast<int64_t>(tc.h) * p.head_pitch + tc.q * 16;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    r[j][0] = r[j][1] = r[j][2] = r[j][3] = 0;
+    if (j < nv) {
+      if (j > 0) cursor_next(p, rc);
+      const int64_t row = cursor_row(p, tc.half, rc);
+      if (row >= 0) {
+        const uint4 x = *reinterpret_cast<const uint4*>(col + row * p.row_pitch);
+        r[j][0] = x.x;
+        r[j][1] = x.y;
+        r[j][2] = x.z;
+        r[j][3] = x.w;
+      }
+    }
+  }
+  uint32_t v[16][4];
+  transpose16(r, v);
+
+  constexpr int NU = (16 * BITS + 31) / 32;
+  const int nbytes = (nv * BITS) >> 3;
+  const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t d = desc[tc.ql * 16 + k];
+    if (d < 0) continue;
+    const int64_t P = d + p.bit_bias + sym0 * BITS;  // byte aligned by plan
+    uint32_t u[NU > 4 ? NU : 4];
+    compress16<BITS>(v[k], u);
+    store_stream<ALIGNED>(p.stream + (P >> 3), u, nbytes);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic kernels (any layout, any plan)
+// ---------------------------------------------------------------------------
+
+struct GenericLayout {
+  int64_t st, sh, sc;  // element strides of the token / head / head_dim axes
+};
+
+// bitpack_layout_cuda.cu:70-89: 16-bit LE window, bytes past the chunk read 0.
+__device__ __forceinline__ uint8_t unpack_symbol(const uint8_t* src, int64_t nbytes,
+                                                 int64_t i, int bits) {
+  if (bits == 8) return src[i];
+  const int64_t bp = i * bits;
+  const int64_t k = bp >> 3;
+  uint32_t w = 0;
+  if (k < nbytes) w = src[k];
+  if (k + 1 < nbytes) w |= static_cast<uint32_t>(src[k + 1]) << 8;
+  return static_cast<uint8_t>((w >> (bp & 7)) & ((1u << bits) - 1u));
+}
+
+__global__ __launch_bounds__(kThreads) void generic_unpack_kernel(
+    const uint8_t* __restrict__ flat, const int64_t* __restrict__ offsets,
+    const int64_t* __restrict__ bits, const int64_t* __restrict__ specs,
+    GenericLayout L, uint8_t* __restrict__ out) {
+  const int64_t k = blockIdx.y;
+  const int64_t* s = specs + 6 * k;
+  const int64_t Tc = s[5] - s[4], Cc = s[3] - s[2];
+  const int64_t per_head = Tc * Cc, n = (s[1] - s[0]) * per_head;
+  const int b = static_cast<int>(bits[k]);
+  const uint8_t* src = flat + offsets[k];
+  const int64_t nbytes = offsets[k + 1] - offsets[k];
+  const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step) {
+    const int64_t hh = i / per_head;
+    const int64_t rem = i - hh * per_head;
+    const int64_t cc = rem / Tc;
+    const int64_t tt = rem - cc * Tc;
+    out[(s[4] + tt) * L.st + (s[0] + hh) * L.sh + (s[2] + cc) * L.sc] =
+        unpack_symbol(src, nbytes, i, b);
+  }
+}
+
+// One thread per output byte: ORs in the (at most 8) symbols overlapping it.
+__global__ __launch_bounds__(kThreads) void generic_pack_kernel(
+    const uint8_t* __restrict__ symbols, const int64_t* __restrict__ offsets,
+    const int64_t* __restrict__ bits, const int64_t* __restrict__ specs,
+    GenericLayout L, uint8_t* __restrict__ flat) {
+  const int64_t k = blockIdx.y;
+  const int64_t* s = specs + 6 * k;
+  const int64_t Tc = s[5] - s[4], Cc = s[3] - s[2];
+  const int64_t per_head = Tc * Cc, n = (s[1] - s[0]) * per_head;
+  const int b = static_cast<int>(bits[k]);
+  const uint32_t mask = (1u << b) - 1u;
+  uint8_t* dst = flat + offsets[k];
+  const int64_t nbytes = offsets[k + 1] - offsets[k];
+  const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t byte = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; byte < nbytes;
+       byte += step) {
+    const int64_t first = (byte * 8) / b;
+    int64_t last = (byte * 8 + 7) / b;
+    if (last > n - 1) last = n - 1;
+    uint32_t acc = 0;
+    for (int64_t i = first; i <= last; ++i) {
+      const int64_t hh = i / per_head;
+      const int64_t rem = i - hh * per_head;
+      const int64_t cc = rem / Tc;
+      const int64_t tt = rem - cc * Tc;
+      const uint32_t sym =
+          symbols[(s[4] + tt) * L.st + (s[0] + hh) * L.sh + (s[2] + cc) * L.sc] & mask;
+      const int64_t shift = i * b - byte * 8;
+      acc |= shift >= 0 ? (sym << shift) : (sym >> (-shift));
+    }
+    dst[byte] = static_cast<uint8_t>(acc & 0xffu);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void fill_zero_kernel(uint8_t* __restrict__ p, int64_t n) {
+  // p is 16-byte aligned by the caller; the tail is written bytewise.
+  const int64_t nvec = n >> 4;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (int64_t i = tid; i < nvec; i += step)
+    reinterpret_cast<uint4*>(p)[i] = make_uint4(0, 0, 0, 0);
+  const int64_t tail = n - (nvec << 4);
+  if (tid < tail) p[(nvec << 4) + tid] = 0;
+}
+
+__global__ __launch_bounds__(kThreads) void fill_zero_bytes_kernel(uint8_t* __restrict__ p, int64_t n) {
+  const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step)
+    p[i] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Paged block copies (token-major K/V <-> cache)
+// ---------------------------------------------------------------------------
+
+struct BlockCopyParams {
+  const uint8_t* src;
+  uint8_t* dst;
+  const int64_t* block_ids;
+  int64_t num_blocks;
+  int64_t T;           // valid tokens per half in the token-major tensor
+  int64_t Tt;          // token-major tokens per half (T for scatter, block_count*bs for gather)
+  int64_t block_count, bs, blk_stride, half_stride;
+  int64_t row_bytes;   // H * head_bytes
+};
+
+// SCATTER: token-major value -> cache rows (zero rows for t >= T).
+// GATHER:  cache rows -> token-major value.
+template <bool SCATTER, int VEC>
+__global__ __launch_bounds__(kThreads) void block_copy_kernel(BlockCopyParams p) {
+  const int64_t vec_per_row = p.row_bytes / VEC;
+  const int64_t rows_per_half = p.block_count * p.bs;
+  const int64_t total = 2 * rows_per_half * vec_per_row;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
+       idx += step) {
+    const int64_t v = idx % vec_per_row;
+    const int64_t r = idx / vec_per_row;
+    const int64_t t = r % rows_per_half;
+    const int64_t half = r / rows_per_half;
+    const int64_t blk = t / p.bs;
+    const int64_t pid = p.block_ids[blk];
+    if (pid < 0 || pid >= p.num_blocks) continue;
+    const int64_t cache_row = pid * p.blk_stride + half * p.half_stride + (t - blk * p.bs);
+    const int64_t cache_off = cache_row * p.row_bytes + v * VEC;
+    if constexpr (SCATTER) {
+      if constexpr (VEC == 16) {
+        uint4 x = make_uint4(0, 0, 0, 0);
+        if (t < p.T) x = *reinterpret_cast<const uint4*>(p.src + (half * p.T + t) * p.row_bytes + v * 16);
+        *reinterpret_cast<uint4*>(p.dst + cache_off) = x;
+      } else {
+        p.dst[cache_off] = t < p.T ? p.src[(half * p.T + t) * p.row_bytes + v] : 0;
+      }
+    } else {
+      const int64_t val_off = (half * p.Tt + t) * p.row_bytes + v * VEC;
+      if constexpr (VEC == 16) {
+        *reinterpret_cast<uint4*>(p.dst + val_off) = *reinterpret_cast<const uint4*>(p.src + cache_off);
+      } else {
+        p.dst[val_off] = p.src[cache_off];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launch helpers
+// ---------------------------------------------------------------------------
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+unsigned grid_for(int64_t work, int64_t per_block, int64_t cap) {
+  int64_t g = (work + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return static_cast<unsigned>(g);
+}
+
+int launch_fill_zero(uint8_t* p, int64_t n, hipStream_t stream) {
+  if (n <= 0) return ORIGAMI_OK;
+  if (aligned16(p)) {
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(grid_for(n >> 4, kThreads, 65536)), dim3(kThreads), 0,
+                       stream, p, n);
+  } else {
+    hipLaunchKernelGGL(fill_zero_bytes_kernel, dim3(grid_for(n, kThreads, 65536)), dim3(kThreads),
+                       0, stream, p, n);
+  }
+  return check_launch("fill_zero_kernel");
+}
+
+// Fills the stream fields of RowsParams: `flat` may have any alignment.
+void set_stream(RowsParams& p, const uint8_t* flat, int64_t flat_bytes) {
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(flat);
+  const uintptr_t base = addr & ~uintptr_t(3);
+  p.stream = reinterpret_cast<uint8_t*>(base);
+  p.bit_bias = static_cast<int64_t>(addr - base) * 8;
+  p.stream_bytes = flat_bytes + static_cast<int64_t>(addr - base);
+}
+
+void set_grid_dims(RowsParams& p, int64_t nhalf, int64_t H, int64_t C, int64_t tile_tokens_total) {
+  p.H = static_cast<int32_t>(H);
+  p.C = C;
+  p.nq = static_cast<int32_t>(C / 16);
+  p.nqg = (p.nq + kLaneGroups - 1) / kLaneGroups;
+  p.nsg_wg = static_cast<int32_t>((tile_tokens_total + kTileTokens - 1) / kTileTokens);
+  (void)nhalf;
+}
+
+int launch_rows(bool pack, const RowsParams& p, int64_t nhalf, int bits, bool aligned,
+                hipStream_t stream) {
+  const int64_t blocks = nhalf * p.H * p.nqg * static_cast<int64_t>(p.nsg_wg);
+  if (blocks <= 0) return ORIGAMI_OK;
+  if (blocks > INT32_MAX) return fail(ORIGAMI_ERR_INVALID, "layer too large for one launch");
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+#define ORIGAMI_ROWS_CASE(B)                                                           \
+  case B:                                                                              \
+    if (pack) {                                                                        \
+      if (B == 8 && aligned)                                                           \
+        hipLaunchKernelGGL((rows_pack_kernel<8, true>), grid, block, 0, stream, p);    \
+      else                                                                             \
+        hipLaunchKernelGGL((rows_pack_kernel<B, false>), grid, block, 0, stream, p);   \
+    } else {                                                                           \
+      if (B == 8 && aligned)                                                           \
+        hipLaunchKernelGGL((rows_unpack_kernel<8, true>), grid, block, 0, stream, p);  \
+      else                                                                             \
+        hipLaunchKernelGGL((rows_unpack_kernel<B, false>), grid, block, 0, stream, p); \
+    }                                                                                  \
+    break;
+  switch (bits) {
+    ORIGAMI_ROWS_CASE(1)
+    ORIGAMI_ROWS_CASE(2)
+    ORIGAMI_ROWS_CASE(3)
+    ORIGAMI_ROWS_CASE(4)
+    ORIGAMI_ROWS_CASE(5)
+    ORIGAMI_ROWS_CASE(6)
+    ORIGAMI_ROWS_CASE(7)
+    ORIGAMI_ROWS_CASE(8)
+    default:
+      return fail(ORIGAMI_ERR_INVALID, "Origami CUDA bitpack supports only 1..8 bit symbols");
+  }
+#undef ORIGAMI_ROWS_CASE
+  return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
+}
+
+int cache_geometry(int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+                   int64_t* blk_stride, int64_t* half_stride) {
+  if (cache_layout == ORIGAMI_CACHE_KV_FIRST) {
+    *blk_stride = block_size;               // [2, NB, bs, H, D]
+    *half_stride = num_blocks * block_size;
+  } else if (cache_layout == ORIGAMI_CACHE_BLOCKS_FIRST) {
+    *blk_stride = 2 * block_size;           // [NB, 2, bs, H, D]
+    *half_stride = block_size;
+  } else {
+    return fail(ORIGAMI_ERR_INVALID,
+                "kv_cache must be [num_blocks,2,block,heads,dim] or [2,num_blocks,block,heads,dim]");
+  }
+  return ORIGAMI_OK;
+}
+
+const int64_t kKvAxes[4] = {0, 1, 2, -1};
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+
+extern "C" {
+
+const char* origami_last_error(void) { return g_last_error.c_str(); }
+
+int origami_abi_version(void) { return 1; }
+
+int origami_validate_chunks(const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
+                            const int64_t* chunk_specs, int64_t num_chunks,
+                            const int64_t* source_shape, int64_t rank,
+                            const int64_t* axis_positions, int64_t token_count,
+                            int64_t num_heads, int64_t head_dim, int64_t flat_bytes) {
+  return validate_layout(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, source_shape,
+                         rank, axis_positions, token_count, num_heads, head_dim, flat_bytes,
+                         nullptr);
+}
+
+int origami_plan_planes(const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
+                        const int64_t* chunk_specs, int64_t num_chunks, int64_t token_count,
+                        int64_t num_heads, int64_t head_dim, int64_t* table, int64_t table_len,
+                        int64_t* info) {
+  ORIGAMI_REQUIRE(token_count > 0 && num_heads > 0 && head_dim > 0,
+                  "canonical symbol shape must be positive");
+  ORIGAMI_REQUIRE(table_len == num_heads * head_dim, "table_len must be num_heads * head_dim");
+  const int64_t shape[3] = {token_count, num_heads, head_dim};
+  const int64_t last = num_chunks > 0 ? chunk_offsets[num_chunks] : 0;
+  int rc = validate_layout(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, shape, 3,
+                           kKvAxes, token_count, num_heads, head_dim, last, nullptr);
+  if (rc) return rc;
+  const PlanInfo pi = build_plane_table(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks,
+                                        token_count, num_heads, head_dim, table);
+  info[0] = pi.regular;
+  info[1] = pi.bits;
+  info[2] = pi.aligned16;
+  info[3] = pi.byte_aligned;
+  return ORIGAMI_OK;
+}
+
+int origami_unpack_canonical_storage_chunks(
+    const uint8_t* flat_chunks, int64_t flat_bytes, const int64_t* chunk_offsets,
+    const int64_t* bits_per_chunk, const int64_t* chunk_specs, int64_t num_chunks,
+    const int64_t* source_shape, int64_t rank, const int64_t* axis_positions,
+    int64_t token_count, int64_t num_heads, int64_t head_dim, uint8_t* output,
+    int64_t output_bytes, origami_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  Strides st;
+  int rc = validate_layout(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, source_shape,
+                           rank, axis_positions, token_count, num_heads, head_dim, flat_bytes,
+                           &st);
+  if (rc) return rc;
+  int64_t total = 1;
+  for (int64_t a = 0; a < rank; ++a) total *= source_shape[a];
+  ORIGAMI_REQUIRE(output_bytes == total, "output size must equal prod(source_shape)");
+  if (num_chunks == 0) return launch_fill_zero(output, output_bytes, stream);
+
+  const int64_t T = token_count, H = num_heads, C = head_dim;
+  const bool rows_layout = st.channel == 1 && C % 16 == 0 && st.token % 16 == 0 &&
+                           st.head % 16 == 0 && aligned16(output) && T >= 16 &&
+                           H * C <= kMaxPlaneTable;
+  const Plan* plan = nullptr;
+  rc = get_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, T, H, C, rows_layout, &plan);
+  if (rc) return rc;
+
+  if (rows_layout && plan->has_table && plan->info.regular && plan->info.bits != 0) {
+    RowsParams p{};
+    set_stream(p, flat_chunks, flat_bytes);
+    p.planes = plan->d_table;
+    p.rows = output;
+    p.block_ids = nullptr;
+    p.num_blocks = 0;
+    p.T = T;
+    p.row_tokens = T;
+    p.row_pitch = st.token;
+    p.head_pitch = st.head;
+    p.bs = T;
+    p.blk_stride = 0;
+    p.half_stride = 0;
+    set_grid_dims(p, 1, H, C, T);
+    const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks);
+    return launch_rows(false, p, 1, plan->info.bits, al, stream);
+  }
+
+  rc = launch_fill_zero(output, output_bytes, stream);
+  if (rc) return rc;
+  const GenericLayout L{st.token, st.head, st.channel};
+  const dim3 grid(grid_for(plan->max_symbols, kThreads, 4096), static_cast<unsigned>(num_chunks));
+  hipLaunchKernelGGL(generic_unpack_kernel, grid, dim3(kThreads), 0, stream, flat_chunks,
+                     plan->d_offsets, plan->d_bits, plan->d_specs, L, output);
+  return check_launch("generic_unpack_kernel");
+}
+
+int origami_pack_canonical_storage_chunks(
+    const uint8_t* symbols, int64_t symbol_bytes, const int64_t* chunk_offsets,
+    const int64_t* bits_per_chunk, const int64_t* chunk_specs, int64_t num_chunks,
+    const int64_t* source_shape, int64_t rank, const int64_t* axis_positions,
+    int64_t token_count, int64_t num_heads, int64_t head_dim, uint8_t* flat_chunks,
+    int64_t flat_bytes, origami_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  Strides st;
+  int rc = validate_layout(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, source_shape,
+                           rank, axis_positions, token_count, num_heads, head_dim, flat_bytes,
+                           &st);
+  if (rc) return rc;
+  int64_t total = 1;
+  for (int64_t a = 0; a < rank; ++a) total *= source_shape[a];
+  ORIGAMI_REQUIRE(symbol_bytes == total, "symbols size must equal prod(source_shape)");
+  if (num_chunks == 0) return ORIGAMI_OK;
+
+  const int64_t T = token_count, H = num_heads, C = head_dim;
+  const bool rows_layout = st.channel == 1 && C % 16 == 0 && st.token % 16 == 0 &&
+                           st.head % 16 == 0 && aligned16(symbols) && T >= 16 &&
+                           H * C <= kMaxPlaneTable;
+  const Plan* plan = nullptr;
+  rc = get_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, T, H, C, rows_layout, &plan);
+  if (rc) return rc;
+
+  if (rows_layout && plan->has_table && plan->info.regular && plan->info.bits != 0 &&
+      plan->info.byte_aligned && (T * plan->info.bits) % 8 == 0) {
+    RowsParams p{};
+    set_stream(p, flat_chunks, flat_bytes);
+    p.planes = plan->d_table;
+    p.rows = const_cast<uint8_t*>(symbols);
+    p.T = T;
+    p.row_tokens = T;
+    p.row_pitch = st.token;
+    p.head_pitch = st.head;
+    p.bs = T;
+    set_grid_dims(p, 1, H, C, T);
+    const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks) && T % 16 == 0;
+    return launch_rows(true, p, 1, plan->info.bits, al, stream);
+  }
+
+  const GenericLayout L{st.token, st.head, st.channel};
+  int64_t max_bytes = 0;
+  for (int64_t k = 0; k < num_chunks; ++k)
+    max_bytes = std::max(max_bytes, chunk_offsets[k + 1] - chunk_offsets[k]);
+  const dim3 grid(grid_for(max_bytes, kThreads, 4096), static_cast<unsigned>(num_chunks));
+  hipLaunchKernelGGL(generic_pack_kernel, grid, dim3(kThreads), 0, stream, symbols,
+                     plan->d_offsets, plan->d_bits, plan->d_specs, L, flat_chunks);
+  return check_launch("generic_pack_kernel");
+}
+
+int origami_unpack_canonical_to_kv_cache(
+    const uint8_t* flat_chunks, int64_t flat_bytes, const int64_t* chunk_offsets,
+    const int64_t* bits_per_chunk, const int64_t* chunk_specs, int64_t num_chunks, int64_t tokens,
+    void* kv_cache, int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+    int64_t num_heads, int64_t head_bytes, const int64_t* block_ids, int64_t block_count,
+    origami_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  ORIGAMI_REQUIRE(tokens > 0 && num_heads > 0 && head_bytes > 0,
+                  "tokens, heads, and head_dim must be positive");
+  ORIGAMI_REQUIRE(block_size > 0, "kv_cache block size must be positive");
+  ORIGAMI_REQUIRE(num_blocks > 0, "kv_cache must hold at least one block");
+  ORIGAMI_REQUIRE(block_count > 0, "block_ids must be non-empty");
+  ORIGAMI_REQUIRE(tokens <= block_count * block_size, "tokens exceed destination block capacity");
+  const int64_t shape[3] = {2 * tokens, num_heads, head_bytes};
+  int rc = validate_layout(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, shape, 3,
+                           kKvAxes, 2 * tokens, num_heads, head_bytes, flat_bytes, nullptr);
+  if (rc) return rc;
+  int64_t blk_stride = 0, half_stride = 0;
+  rc = cache_geometry(cache_layout, num_blocks, block_size, &blk_stride, &half_stride);
+  if (rc) return rc;
+  if (head_bytes % 16 != 0 || !aligned16(kv_cache) ||
+      num_heads * head_bytes > kMaxPlaneTable)
+    return fail(ORIGAMI_ERR_UNSUPPORTED, "fused restore needs 16-byte head rows");
+  const Plan* plan = nullptr;
+  rc = get_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, 2 * tokens, num_heads,
+                head_bytes, true, &plan);
+  if (rc) return rc;
+  if (!plan->has_table || !plan->info.regular || plan->info.bits == 0)
+    return fail(ORIGAMI_ERR_UNSUPPORTED,
+                "fused restore needs chunks spanning all tokens with one bit width");
+  RowsParams p{};
+  set_stream(p, flat_chunks, flat_bytes);
+  p.planes = plan->d_table;
+  p.rows = static_cast<uint8_t*>(kv_cache);
+  p.block_ids = block_ids;
+  p.num_blocks = num_blocks;
+  p.T = tokens;
+  p.row_tokens = block_count * block_size;
+  p.row_pitch = num_heads * head_bytes;
+  p.head_pitch = head_bytes;
+  p.bs = block_size;
+  p.blk_stride = blk_stride;
+  p.half_stride = half_stride;
+  set_grid_dims(p, 2, num_heads, head_bytes, p.row_tokens);
+  const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks) &&
+                  tokens % 16 == 0;
+  return launch_rows(false, p, 2, plan->info.bits, al, stream);
+}
+
+int origami_pack_canonical_from_kv_cache(
+    const void* kv_cache, int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+    int64_t num_heads, int64_t head_bytes, const int64_t* block_ids, int64_t block_count,
+    int64_t tokens, const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
+    const int64_t* chunk_specs, int64_t num_chunks, uint8_t* flat_chunks, int64_t flat_bytes,
+    origami_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  ORIGAMI_REQUIRE(tokens > 0 && num_heads > 0 && head_bytes > 0,
+                  "tokens, heads, and head_dim must be positive");
+  ORIGAMI_REQUIRE(block_size > 0, "kv_cache block size must be positive");
+  ORIGAMI_REQUIRE(num_blocks > 0, "kv_cache must hold at least one block");
+  ORIGAMI_REQUIRE(block_count > 0, "block_ids must be non-empty");
+  ORIGAMI_REQUIRE(tokens <= block_count * block_size, "tokens exceed source block capacity");
+  const int64_t shape[3] = {2 * tokens, num_heads, head_bytes};
+  int rc = validate_layout(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, shape, 3,
+                           kKvAxes, 2 * tokens, num_heads, head_bytes, flat_bytes, nullptr);
+  if (rc) return rc;
+  int64_t blk_stride = 0, half_stride = 0;
+  rc = cache_geometry(cache_layout, num_blocks, block_size, &blk_stride, &half_stride);
+  if (rc) return rc;
+  if (head_bytes % 16 != 0 || !aligned16(kv_cache) ||
+      num_heads * head_bytes > kMaxPlaneTable)
+    return fail(ORIGAMI_ERR_UNSUPPORTED, "fused save needs 16-byte head rows");
+  const Plan* plan = nullptr;
+  rc = get_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, 2 * tokens, num_heads,
+                head_bytes, true, &plan);
+  if (rc) return rc;
+  if (!plan->has_table || !plan->info.regular || plan->info.bits == 0 ||
+      !plan->info.byte_aligned || (tokens * plan->info.bits) % 8 != 0)
+    return fail(ORIGAMI_ERR_UNSUPPORTED,
+                "fused save needs regular byte-aligned planes with one bit width");
+  RowsParams p{};
+  set_stream(p, flat_chunks, flat_bytes);
+  p.planes = plan->d_table;
+  p.rows = static_cast<uint8_t*>(const_cast<void*>(kv_cache));
+  p.block_ids = block_ids;
+  p.num_blocks = num_blocks;
+  p.T = tokens;
+  p.row_tokens = block_count * block_size;
+  p.row_pitch = num_heads * head_bytes;
+  p.head_pitch = head_bytes;
+  p.bs = block_size;
+  p.blk_stride = blk_stride;
+  p.half_stride = half_stride;
+  set_grid_dims(p, 2, num_heads, head_bytes, tokens);
+  const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks) &&
+                  tokens % 16 == 0;
+  return launch_rows(true, p, 2, plan->info.bits, al, stream);
+}
+
+static int block_copy(bool scatter, const uint8_t* src, uint8_t* dst, int64_t tokens,
+                      int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+                      int64_t num_heads, int64_t head_bytes, const int64_t* block_ids,
+                      int64_t block_count, hipStream_t stream) {
+  ORIGAMI_REQUIRE(num_heads > 0 && head_bytes > 0, "heads and head_dim must be positive");
+  ORIGAMI_REQUIRE(block_size > 0, "kv_cache block size must be positive");
+  ORIGAMI_REQUIRE(num_blocks > 0, "kv_cache must hold at least one block");
+  ORIGAMI_REQUIRE(block_count >= 0, "block count must be non-negative");
+  ORIGAMI_REQUIRE(tokens >= 0 && tokens <= block_count * block_size,
+                  "tokens exceed destination block capacity");
+  if (block_count == 0) return ORIGAMI_OK;
+  BlockCopyParams p{};
+  p.src = src;
+  p.dst = dst;
+  p.block_ids = block_ids;
+  p.num_blocks = num_blocks;
+  p.T = tokens;
+  p.Tt = block_count * block_size;
+  p.block_count = block_count;
+  p.bs = block_size;
+  p.row_bytes = num_heads * head_bytes;
+  int rc = cache_geometry(cache_layout, num_blocks, block_size, &p.blk_stride, &p.half_stride);
+  if (rc) return rc;
+  const bool vec = p.row_bytes % 16 == 0 && aligned16(src) && aligned16(dst);
+  const int64_t work = 2 * p.Tt * (vec ? p.row_bytes / 16 : p.row_bytes);
+  const dim3 grid(grid_for(work, kThreads, 65536)), block(kThreads);
+  if (scatter) {
+    if (vec)
+      hipLaunchKernelGGL((block_copy_kernel<true, 16>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((block_copy_kernel<true, 1>), grid, block, 0, stream, p);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((block_copy_kernel<false, 16>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((block_copy_kernel<false, 1>), grid, block, 0, stream, p);
+  }
+  return check_launch("block_copy_kernel");
+}
+
+int origami_scatter_kv_blocks(const uint8_t* value, int64_t tokens, void* kv_cache,
+                              int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+                              int64_t num_heads, int64_t head_bytes, const int64_t* block_ids,
+                              int64_t block_count, origami_stream_t stream) {
+  return block_copy(true, value, static_cast<uint8_t*>(kv_cache), tokens, cache_layout,
+                    num_blocks, block_size, num_heads, head_bytes, block_ids, block_count,
+                    reinterpret_cast<hipStream_t>(stream));
+}
+
+int origami_gather_kv_blocks(const void* kv_cache, int64_t cache_layout, int64_t num_blocks,
+                             int64_t block_size, int64_t num_heads, int64_t head_bytes,
+                             const int64_t* block_ids, int64_t block_count, uint8_t* value,
+                             origami_stream_t stream) {
+  return block_copy(false, static_cast<const uint8_t*>(kv_cache), value,
+                    block_count * block_size, cache_layout, num_blocks, block_size, num_heads,
+                    head_bytes, block_ids, block_count, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,404 @@
+"""GPU layout path: Python front end of liborigami_layout.so.
+
+Mirrors lossless/native_gpu.py of the reference (load_bitpack_cuda_extension,
+available, unpack_canonical_storage_chunks; native_gpu.py:35-146) and adds the
+pieces the reference lacks: the pack, the fused unpack+scatter into the paged
+KV cache and the fused gather+pack from it.
+
+All work is enqueued on the calling thread's current stream of the tensors'
+device, like the reference (bitpack_layout_cuda.cpp:370).  Chunk metadata stays
+on the host: no call reads device memory back.
+"""
+from __future__ import annotations
+
+import ctypes
+from functools import lru_cache
+from typing import Any, Iterable, Sequence
+
+import numpy as np
+import torch
+
+from origami_amd import _native
+from origami_amd.layout import CanonicalLayout, kv_symbol_layout
+
+CACHE_KV_FIRST = _native.CACHE_KV_FIRST
+CACHE_BLOCKS_FIRST = _native.CACHE_BLOCKS_FIRST
+
+
+def _stream_handle(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_cuda(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def available() -> bool:
+    """True when a GPU is visible and the native library loads."""
+    if not torch.cuda.is_available():
+        return False
+    try:
+        _native.lib()
+        return True
+    except Exception:  # noqa: BLE001 - mirrors the reference's available()
+        return False
+
+
+# ---------------------------------------------------------------------------
+# Flat streams
+# ---------------------------------------------------------------------------
+
+def flat_chunks_and_offsets(chunks: Iterable[torch.Tensor] | torch.Tensor,
+                            device: torch.device) -> tuple[torch.Tensor, list[int]]:
+    """Concatenates chunk tensors on `device` (native_gpu.py:92-110)."""
+    if isinstance(chunks, torch.Tensor):
+        flat = chunks.detach().reshape(-1)
+        if flat.device != device or flat.dtype != torch.uint8:
+            flat = flat.to(device=device, dtype=torch.uint8, non_blocking=True)
+        return flat.contiguous(), [0, int(flat.numel())]
+    parts, offsets, total = [], [0], 0
+    for chunk in chunks:
+        part = chunk.detach().reshape(-1).to(device=device, dtype=torch.uint8, non_blocking=True)
+        parts.append(part)
+        total += int(part.numel())
+        offsets.append(total)
+    if not parts:
+        return torch.empty((0,), dtype=torch.uint8, device=device), offsets
+    flat = parts[0] if len(parts) == 1 else torch.cat(parts)
+    return flat.contiguous(), offsets
+
+
+def _layout_args(layout: CanonicalLayout) -> tuple:
+    return (
+        _native.host_ptr(layout.offsets), _native.host_ptr(layout.bits),
+        _native.host_ptr(layout.specs), layout.num_chunks,
+    )
+
+
+# ---------------------------------------------------------------------------
+# Canonical pack / unpack (source-layout symbol tensors)
+# ---------------------------------------------------------------------------
+
+def unpack_layout(flat: torch.Tensor, layout: CanonicalLayout,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """Unpacks a flat stream into a new (or given) uint8 symbol tensor."""
+    _require_cuda(flat, "flat_chunks")
+    if flat.dtype != torch.uint8:
+        raise RuntimeError("flat_chunks must be uint8")
+    if out is None:
+        out = torch.empty((layout.symbol_count,), dtype=torch.uint8, device=flat.device)
+    _require_cuda(out, "output")
+    with torch.cuda.device(flat.device):
+        _native.call(
+            "origami_unpack_canonical_storage_chunks",
+            flat.data_ptr(), flat.numel(), *_layout_args(layout),
+            _native.host_ptr(layout.shape_arr), len(layout.shape), _native.host_ptr(layout.axes),
+            layout.token_count, layout.num_heads, layout.head_dim,
+            out.data_ptr(), out.numel(), _stream_handle(flat.device))
+    return out
+
+
+def pack_layout(symbols: torch.Tensor, layout: CanonicalLayout,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Packs a uint8 symbol tensor into a new (or given) flat stream."""
+    _require_cuda(symbols, "symbols")
+    if symbols.dtype != torch.uint8:
+        raise RuntimeError("symbols must be uint8")
+    if out is None:
+        out = torch.empty((layout.stream_bytes,), dtype=torch.uint8, device=symbols.device)
+    _require_cuda(out, "flat_chunks")
+    with torch.cuda.device(symbols.device):
+        _native.call(
+            "origami_pack_canonical_storage_chunks",
+            symbols.data_ptr(), symbols.numel(), *_layout_args(layout),
+            _native.host_ptr(layout.shape_arr), len(layout.shape), _native.host_ptr(layout.axes),
+            layout.token_count, layout.num_heads, layout.head_dim,
+            out.data_ptr(), out.numel(), _stream_handle(symbols.device))
+    return out
+
+
+def unpack_canonical_storage_chunks(
+    chunks: Iterable[torch.Tensor] | torch.Tensor,
+    bits: int | Sequence[int],
+    source_shape: Sequence[int],
+    source_layout: Sequence[str],
+    chunk_specs,
+    *,
+    device: torch.device | str | None = None,
+) -> torch.Tensor:
+    """Same contract as the reference (native_gpu.py:113-146): returns the
+    flat uint8 symbol tensor of prod(source_shape) bytes on `device`."""
+    target = torch.device(device or "cuda")
+    if target.type == "cuda" and target.index is None:
+        target = torch.device("cuda", torch.cuda.current_device())
+    layout = CanonicalLayout.make(source_shape, source_layout, bits, chunk_specs)
+    flat, offsets = flat_chunks_and_offsets(chunks, target)
+    if not isinstance(chunks, torch.Tensor) and len(offsets) - 1 != layout.num_chunks:
+        raise RuntimeError("Origami native layout metadata chunk count does not match payload chunks")
+    if not isinstance(chunks, torch.Tensor) and not np.array_equal(
+            np.asarray(offsets, dtype=np.int64), layout.offsets):
+        raise RuntimeError("Origami CUDA packed chunk byte size mismatch")
+    return unpack_layout(flat, layout)
+
+
+def pack_canonical_storage_flat(
+    symbols: torch.Tensor,
+    bits: int | Sequence[int],
+    source_shape: Sequence[int],
+    source_layout: Sequence[str],
+    chunk_specs,
+) -> tuple[torch.Tensor, CanonicalLayout]:
+    """Packs on the symbols' device; returns (flat stream, layout)."""
+    layout = CanonicalLayout.make(source_shape, source_layout, bits, chunk_specs)
+    flat_symbols = symbols.detach().reshape(-1)
+    if flat_symbols.dtype != torch.uint8:
+        flat_symbols = flat_symbols.to(torch.uint8)
+    return pack_layout(flat_symbols.contiguous(), layout), layout
+
+
+def pack_canonical_storage_chunks(
+    symbols: torch.Tensor,
+    bits: int | Sequence[int],
+    source_shape: Sequence[int],
+    source_layout: Sequence[str],
+    chunk_specs,
+) -> list[torch.Tensor]:
+    """The packer the reference leaves as a stub (native_cpu.py:144-151):
+    returns one uint8 tensor per chunk spec (views of one device stream)."""
+    flat, layout = pack_canonical_storage_flat(symbols, bits, source_shape, source_layout,
+                                               chunk_specs)
+    off = layout.offsets
+    return [flat[int(off[k]):int(off[k + 1])] for k in range(layout.num_chunks)]
+
+
+# ---------------------------------------------------------------------------
+# Paged KV cache
+# ---------------------------------------------------------------------------
+
+def cache_geometry(kv_cache: torch.Tensor, num_heads: int | None = None,
+                   head_dim: int | None = None) -> tuple[int, int, int, int, int]:
+    """(layout code, num_blocks, block_size, heads, head_bytes) of a rank-5
+    paged cache.  [2, NB, bs, H, D] is recognised first (the rule of
+    benchmark_utils.py:357 and bitpack_layout_cuda.cpp:810-831), then
+    [NB, 2, bs, H, D]."""
+    if kv_cache.dim() != 5:
+        raise RuntimeError("kv_cache must have rank 5")
+    if kv_cache.shape[0] == 2:
+        code, nb = CACHE_KV_FIRST, int(kv_cache.shape[1])
+    elif kv_cache.shape[1] == 2:
+        code, nb = CACHE_BLOCKS_FIRST, int(kv_cache.shape[0])
+    else:
+        raise RuntimeError("kv_cache must be [num_blocks,2,block,heads,dim] or "
+                           "[2,num_blocks,block,heads,dim]")
+    bs, H, D = (int(x) for x in kv_cache.shape[2:])
+    if num_heads is not None and head_dim is not None and (H != num_heads or D != head_dim):
+        raise RuntimeError("kv_cache head shape mismatch")
+    return code, nb, bs, H, D * kv_cache.element_size()
+
+
+def block_ids_tensor(block_ids, device: torch.device, num_blocks: int | None = None
+                     ) -> torch.Tensor:
+    """int64 device block table; ids are validated on the host first."""
+    if isinstance(block_ids, torch.Tensor):
+        ids_cpu = block_ids.detach().to("cpu", torch.int64)
+    else:
+        ids_cpu = torch.tensor([int(b) for b in block_ids], dtype=torch.int64)
+    if ids_cpu.numel() == 0:
+        raise RuntimeError("block_ids must be non-empty")
+    if num_blocks is not None and (int(ids_cpu.min()) < 0 or int(ids_cpu.max()) >= num_blocks):
+        raise RuntimeError("block id out of range for kv_cache")
+    if isinstance(block_ids, torch.Tensor) and block_ids.device == device \
+            and block_ids.dtype == torch.int64 and block_ids.is_contiguous():
+        return block_ids
+    return ids_cpu.to(device).contiguous()
+
+
+def unpack_to_kv_cache(flat: torch.Tensor, layout: CanonicalLayout, tokens: int,
+                       kv_cache: torch.Tensor, block_ids: torch.Tensor) -> None:
+    """Fused restore of one layer: stream -> paged cache through the block
+    table.  `layout` is the [2*tokens, H, head_bytes] symbol layout of the
+    layer (kv_symbol_layout).  Falls back to unpack + scatter (both on the
+    GPU) when the chunk plan is not served by the fused kernel."""
+    _require_cuda(flat, "flat_chunks")
+    _require_cuda(kv_cache, "kv_cache")
+    _require_cuda(block_ids, "block_ids")
+    code, nb, bs, H, head_bytes = cache_geometry(kv_cache)
+    if layout.token_count != 2 * tokens or layout.num_heads != H or layout.head_dim != head_bytes:
+        raise RuntimeError("symbol layout does not match the kv_cache geometry")
+    with torch.cuda.device(kv_cache.device):
+        try:
+            _native.call(
+                "origami_unpack_canonical_to_kv_cache",
+                flat.data_ptr(), flat.numel(), *_layout_args(layout), int(tokens),
+                kv_cache.data_ptr(), code, nb, bs, H, head_bytes,
+                block_ids.data_ptr(), block_ids.numel(), _stream_handle(kv_cache.device))
+            return
+        except _native.OrigamiNativeError as err:
+            if err.code != _native.ORIGAMI_ERR_UNSUPPORTED:
+                raise
+        # Irregular chunk plan: unpack to the symbol tensor, then scatter.
+        symbols = unpack_layout(flat, layout) if layout.layout == ("token", "head", "head_dim") \
+            else _unpack_kv_tokens_major(flat, layout)
+        scatter_kv_blocks(symbols, tokens, kv_cache, block_ids)
+
+
+def _unpack_kv_tokens_major(flat: torch.Tensor, layout: CanonicalLayout) -> torch.Tensor:
+    """Unpack in any source layout, then permute to token-major bytes."""
+    sym = unpack_layout(flat, layout).reshape(layout.shape)
+    order = [int(layout.axes[0]), int(layout.axes[1]), int(layout.axes[2])]
+    if layout.axes[3] >= 0:
+        sym = sym.squeeze(int(layout.axes[3]))
+        order = [a - (1 if a > layout.axes[3] else 0) for a in order]
+    return sym.permute(*order).contiguous().reshape(-1)
+
+
+def pack_from_kv_cache(kv_cache: torch.Tensor, block_ids: torch.Tensor, tokens: int,
+                       layout: CanonicalLayout, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused save of one layer: paged cache -> stream.  Falls back to gather +
+    pack (both on the GPU) when the plan is not served by the fused kernel."""
+    _require_cuda(kv_cache, "kv_cache")
+    _require_cuda(block_ids, "block_ids")
+    code, nb, bs, H, head_bytes = cache_geometry(kv_cache)
+    if layout.token_count != 2 * tokens or layout.num_heads != H or layout.head_dim != head_bytes:
+        raise RuntimeError("symbol layout does not match the kv_cache geometry")
+    if out is None:
+        out = torch.empty((layout.stream_bytes,), dtype=torch.uint8, device=kv_cache.device)
+    with torch.cuda.device(kv_cache.device):
+        try:
+            _native.call(
+                "origami_pack_canonical_from_kv_cache",
+                kv_cache.data_ptr(), code, nb, bs, H, head_bytes,
+                block_ids.data_ptr(), block_ids.numel(), int(tokens),
+                *_layout_args(layout), out.data_ptr(), out.numel(),
+                _stream_handle(kv_cache.device))
+            return out
+        except _native.OrigamiNativeError as err:
+            if err.code != _native.ORIGAMI_ERR_UNSUPPORTED:
+                raise
+        value = gather_kv_blocks(kv_cache, block_ids)
+        nblk_tokens = block_ids.numel() * bs
+        value = value.reshape(2, nblk_tokens, H * head_bytes)[:, :tokens].contiguous()
+        if layout.layout != ("token", "head", "head_dim"):
+            value = _tokens_major_to_layout(value.reshape(-1), layout)
+        return pack_layout(value.reshape(-1), layout, out)
+
+
+def _tokens_major_to_layout(value: torch.Tensor, layout: CanonicalLayout) -> torch.Tensor:
+    T, H, C = layout.token_count, layout.num_heads, layout.head_dim
+    tmaj = value.reshape(T, H, C)
+    names = [n for n in layout.layout if n != "layer"]
+    src = {"token": 0, "head": 1, "head_dim": 2}
+    out = tmaj.permute(*[src[n] for n in names]).contiguous()
+    return out.reshape(-1)
+
+
+def scatter_kv_blocks(value: torch.Tensor, tokens: int, kv_cache: torch.Tensor,
+                      block_ids: torch.Tensor) -> None:
+    """Token-major K/V bytes [2, tokens, H, head_bytes] -> paged cache,
+    zero-padding the last block (benchmark_utils.py:350-444)."""
+    _require_cuda(value, "value")
+    _require_cuda(kv_cache, "kv_cache")
+    _require_cuda(block_ids, "block_ids")
+    code, nb, bs, H, head_bytes = cache_geometry(kv_cache)
+    if value.numel() * value.element_size() != 2 * tokens * H * head_bytes:
+        raise RuntimeError("value size does not match 2 * tokens * heads * head_dim")
+    with torch.cuda.device(kv_cache.device):
+        _native.call("origami_scatter_kv_blocks", value.data_ptr(), int(tokens),
+                     kv_cache.data_ptr(), code, nb, bs, H, head_bytes,
+                     block_ids.data_ptr(), block_ids.numel(), _stream_handle(kv_cache.device))
+
+
+def gather_kv_blocks(kv_cache: torch.Tensor, block_ids: torch.Tensor,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Paged cache -> token-major bytes [2, nblk*bs, H, head_bytes] (uint8)."""
+    _require_cuda(kv_cache, "kv_cache")
+    _require_cuda(block_ids, "block_ids")
+    code, nb, bs, H, head_bytes = cache_geometry(kv_cache)
+    n = 2 * block_ids.numel() * bs * H * head_bytes
+    if out is None:
+        out = torch.empty((n,), dtype=torch.uint8, device=kv_cache.device)
+    with torch.cuda.device(kv_cache.device):
+        _native.call("origami_gather_kv_blocks", kv_cache.data_ptr(), code, nb, bs, H,
+                     head_bytes, block_ids.data_ptr(), block_ids.numel(), out.data_ptr(),
+                     _stream_handle(kv_cache.device))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Reference extension surface (origami_bitpack_cuda_v6, cpp:894-903)
+# ---------------------------------------------------------------------------
+
+class _Extension:
+    """The function names the reference extension module exports."""
+
+    @staticmethod
+    def unpack_canonical_storage_chunks_cuda(
+        flat_chunks: torch.Tensor, chunk_offsets: torch.Tensor, bits_per_chunk: torch.Tensor,
+        source_shape: torch.Tensor, axis_positions: torch.Tensor, token_count: int,
+        num_heads: int, head_dim: int, chunk_specs: torch.Tensor,
+    ) -> torch.Tensor:
+        """Signature of bitpack_layout_cuda.cpp:316-325.  Metadata tensors may
+        live on any device (host copies are taken once per call)."""
+        _require_cuda(flat_chunks, "flat_chunks")
+        shape = [int(x) for x in source_shape.reshape(-1).tolist()]
+        axes = [int(x) for x in axis_positions.reshape(-1).tolist()]
+        if len(axes) != 4:
+            raise RuntimeError(
+                "axis_positions must be [token_axis, head_axis, head_dim_axis, layer_axis]")
+        names = ["?"] * len(shape)
+        for name, pos in zip(("token", "head", "head_dim", "layer"), axes):
+            if 0 <= pos < len(names):
+                names[pos] = name
+        if "?" in names:
+            raise RuntimeError("token axis must be present in source layout")
+        offsets = np.ascontiguousarray(chunk_offsets.detach().to("cpu", torch.int64).numpy())
+        bits = [int(b) for b in bits_per_chunk.detach().to("cpu").tolist()]
+        layout = CanonicalLayout.make(shape, names, bits, chunk_specs)
+        if (layout.token_count, layout.num_heads, layout.head_dim) != (
+                int(token_count), int(num_heads), int(head_dim)):
+            raise RuntimeError("source axis sizes must match token_count/num_heads/head_dim")
+        if offsets.shape != layout.offsets.shape:
+            raise RuntimeError("chunk_offsets length must be chunk count + 1")
+        if not np.array_equal(np.diff(offsets), np.diff(layout.offsets)):
+            raise RuntimeError("Origami CUDA packed chunk byte size mismatch")
+        base = int(offsets[0]) if offsets.size else 0
+        flat = flat_chunks.reshape(-1)[base:]
+        return unpack_layout(flat, layout)
+
+    @staticmethod
+    def cachegen_unpack_dequantize_to_kv_cache_cuda(*args: Any, **kwargs: Any) -> None:
+        raise NotImplementedError("CacheGen dequantize-to-cache is not part of this build yet")
+
+    @staticmethod
+    def kivi_dequantize_to_kv_cache_cuda(*args: Any, **kwargs: Any) -> None:
+        raise NotImplementedError("KIVI dequantize-to-cache is not part of this build yet")
+
+    @staticmethod
+    def cachegen_unpack_dequantize_cuda(*args: Any, **kwargs: Any) -> torch.Tensor:
+        raise NotImplementedError("CacheGen unpack-dequantize is not part of this build yet")
+
+    @staticmethod
+    def fused_prefix_attention_cuda(*args: Any, **kwargs: Any) -> None:
+        raise NotImplementedError("fused prefix attention is outside the layout path")
+
+
+@lru_cache(maxsize=1)
+def load_bitpack_cuda_extension() -> _Extension:
+    """Counterpart of native_gpu.load_bitpack_cuda_extension (py:35-49): the
+    AOT-built HIP library instead of a JIT-built CUDA extension."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("Origami HIP layout library requires a ROCm GPU")
+    _native.lib()
+    return _Extension()
+
+
+__all__ = [
+    "available", "load_bitpack_cuda_extension", "flat_chunks_and_offsets",
+    "unpack_canonical_storage_chunks", "pack_canonical_storage_chunks",
+    "pack_canonical_storage_flat", "unpack_layout", "pack_layout", "cache_geometry",
+    "block_ids_tensor", "unpack_to_kv_cache", "pack_from_kv_cache", "scatter_kv_blocks",
+    "gather_kv_blocks", "kv_symbol_layout", "CACHE_KV_FIRST", "CACHE_BLOCKS_FIRST",
+]

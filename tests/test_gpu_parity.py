@@ -1,0 +1,300 @@
+"""Parity of the HIP layout path (liborigami_layout.so) with the CPU oracle.
+
+Every comparison is bit-exact (integer/byte work).  Cases cover bits 1..8,
+five source layouts, regular (planner) and irregular (token-split, partial)
+chunk plans, both paged-cache layouts, ragged token counts, unaligned stream
+pointers, and one full Llama-3-8B layer (32768 tokens) compared whole.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from origami_amd.layout import CanonicalLayout, kv_symbol_layout
+from origami_amd.lossless import native_cpu, native_gpu
+from origami_amd.lossless.chunking import plan_head_channel_chunks
+from tests import bitref
+
+pytestmark = pytest.mark.gpu
+
+LAYOUTS = [
+    (["token", "head", "head_dim"], [0, 1, 2, -1]),
+    (["head", "token", "head_dim"], [1, 0, 2, -1]),
+    (["head", "head_dim", "token"], [2, 0, 1, -1]),
+    (["layer", "token", "head", "head_dim"], [1, 2, 3, 0]),
+    (["token", "layer", "head_dim", "head"], [0, 3, 2, 1]),
+]
+
+
+def _shape(layout, T, H, C):
+    return [{"token": T, "head": H, "head_dim": C, "layer": 1}[a] for a in layout]
+
+
+def planner_specs(T, H, C, target):
+    return np.asarray([[c.layout.head_start, c.layout.head_end, c.layout.channel_start,
+                        c.layout.channel_end, c.layout.token_start, c.layout.token_end]
+                       for c in plan_head_channel_chunks(
+                           layer_index=0, num_heads=H, head_dim=C, token_count=T,
+                           bytes_per_symbol=1, min_bytes=target, target_bytes=target,
+                           max_bytes=target)], dtype=np.int64)
+
+
+def _gpu_u8(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _case_specs(kind, rng, T, H, C):
+    if kind == "planner":
+        return planner_specs(T, H, C, max(64, T * C // 3))
+    if kind == "partition":
+        return bitref.random_specs(rng, T, H, C, partition=True)
+    if kind == "partial":  # a single box: the rest of the tensor is uncovered
+        return np.asarray([[0, H, C // 4, C, 0, T]], np.int64)
+    raise AssertionError(kind)
+
+
+@pytest.mark.parametrize("kind", ["planner", "partition", "partial"])
+@pytest.mark.parametrize("bits", range(1, 9))
+@pytest.mark.parametrize("li", range(len(LAYOUTS)))
+def test_unpack_and_pack_match_oracle(cuda_device, li, bits, kind):
+    layout, axes = LAYOUTS[li]
+    rng = np.random.default_rng(1000 * li + 10 * bits + len(kind))
+    for T, H, C in [(40, 2, 32), (257, 3, 48), (96, 1, 16)]:
+        shape = _shape(layout, T, H, C)
+        specs = _case_specs(kind, rng, T, H, C)
+        sym = rng.integers(0, 256, int(np.prod(shape)), dtype=np.uint8)
+        ref_flat, offs = oracle.pack_canonical(sym, bits, specs, shape, axes)
+        ref_sym = oracle.unpack_canonical(ref_flat, offs, bits, specs, shape, axes)
+
+        flat_gpu, lay = native_gpu.pack_canonical_storage_flat(
+            _gpu_u8(sym, cuda_device), bits, shape, layout, specs)
+        assert np.array_equal(lay.offsets, offs)
+        assert np.array_equal(flat_gpu.cpu().numpy(), ref_flat), (T, H, C)
+
+        out = native_gpu.unpack_canonical_storage_chunks(
+            _gpu_u8(ref_flat, cuda_device), bits, shape, layout, specs, device=cuda_device)
+        assert np.array_equal(out.cpu().numpy(), ref_sym), (T, H, C)
+
+
+@pytest.mark.parametrize("shift", [1, 2, 3, 5])
+@pytest.mark.parametrize("bits", [8, 3])
+def test_unaligned_stream_pointer(cuda_device, shift, bits):
+    rng = np.random.default_rng(shift)
+    T, H, C = 64, 2, 32
+    specs = planner_specs(T, H, C, 1024)
+    sym = rng.integers(0, 256, T * H * C, dtype=np.uint8)
+    ref_flat, offs = oracle.pack_canonical(sym, bits, specs, [T, H, C], [0, 1, 2, -1])
+    buf = torch.zeros(ref_flat.size + 16, dtype=torch.uint8, device=cuda_device)
+    buf[shift:shift + ref_flat.size] = _gpu_u8(ref_flat, cuda_device)
+    view = buf[shift:shift + ref_flat.size]
+    lay = CanonicalLayout.make([T, H, C], ["token", "head", "head_dim"], bits, specs)
+    out = native_gpu.unpack_layout(view, lay)
+    assert np.array_equal(out.cpu().numpy(), sym & ((1 << bits) - 1))
+    # pack into an unaligned destination; the bytes around it stay untouched
+    buf2 = torch.full((ref_flat.size + 16,), 0xAB, dtype=torch.uint8, device=cuda_device)
+    native_gpu.pack_layout(_gpu_u8(sym, cuda_device), lay, buf2[shift:shift + ref_flat.size])
+    host = buf2.cpu().numpy()
+    assert np.array_equal(host[shift:shift + ref_flat.size], ref_flat)
+    assert (host[:shift] == 0xAB).all() and (host[shift + ref_flat.size:] == 0xAB).all()
+
+
+def test_empty_chunk_list_gives_zeros(cuda_device):
+    out = native_gpu.unpack_canonical_storage_chunks(
+        [], 8, [5, 2, 3], ["token", "head", "head_dim"], [], device=cuda_device)
+    assert out.numel() == 30 and int(out.sum()) == 0
+
+
+def _kv_case(rng, tokens, H, C, bs, blocks_first, extra_blocks=5):
+    nblk = -(-tokens // bs)
+    NB = nblk + extra_blocks
+    ids = rng.permutation(NB)[:nblk].astype(np.int64)
+    shape = (NB, 2, bs, H, C) if blocks_first else (2, NB, bs, H, C)
+    cache = rng.integers(0, 256, shape, dtype=np.uint8)
+    return ids, cache
+
+
+@pytest.mark.parametrize("blocks_first", [False, True])
+@pytest.mark.parametrize("bits", [8, 4, 3, 1])
+@pytest.mark.parametrize("tokens,H,C,bs", [
+    (4096, 8, 256, 16),    # Llama-3-8B bf16 geometry, 4096 tokens
+    (1000, 8, 256, 16),    # ragged: last block partially filled
+    (777, 4, 256, 32),     # Qwen2.5-7B heads, ragged, larger blocks
+    (2048, 8, 128, 16),    # fp8 head bytes
+    (100, 2, 64, 8),       # blocks smaller than a lane's 16 tokens
+])
+def test_restore_to_kv_cache_matches_oracle(cuda_device, tokens, H, C, bs, blocks_first, bits):
+    rng = np.random.default_rng(tokens + bits + 7 * bs)
+    specs = planner_specs(2 * tokens, H, C, 1 << 16)
+    value = rng.integers(0, 256, (2, tokens, H, C), dtype=np.uint8)
+    sym = value.reshape(-1)
+    flat, offs = oracle.pack_canonical(sym, bits, specs, [2 * tokens, H, C], [0, 1, 2, -1])
+    ids, cache = _kv_case(rng, tokens, H, C, bs, blocks_first)
+    expect = cache.copy()
+    oracle.restore_layer(flat, offs, bits, specs, tokens, H, C, ids, expect, blocks_first)
+
+    cache_gpu = _gpu_u8(cache, cuda_device)
+    lay = kv_symbol_layout(tokens, H, C, bits, specs)
+    ids_gpu = native_gpu.block_ids_tensor(ids, cuda_device, cache.shape[1 if not blocks_first else 0])
+    native_gpu.unpack_to_kv_cache(_gpu_u8(flat, cuda_device), lay, tokens, cache_gpu, ids_gpu)
+    assert np.array_equal(cache_gpu.cpu().numpy(), expect)
+
+
+@pytest.mark.parametrize("blocks_first", [False, True])
+@pytest.mark.parametrize("bits", [8, 4, 2])
+@pytest.mark.parametrize("tokens,H,C,bs", [
+    (4096, 8, 256, 16), (1000, 8, 256, 16), (2048, 8, 128, 16), (100, 2, 64, 8),
+])
+def test_save_from_kv_cache_matches_oracle(cuda_device, tokens, H, C, bs, blocks_first, bits):
+    rng = np.random.default_rng(tokens * 3 + bits)
+    specs = planner_specs(2 * tokens, H, C, 1 << 16)
+    ids, cache = _kv_case(rng, tokens, H, C, bs, blocks_first)
+    nblk = ids.size
+    gathered = oracle.gather_kv_cache(cache, ids, blocks_first).reshape(2, nblk * bs, H, C)
+    sym = np.ascontiguousarray(gathered[:, :tokens]).reshape(-1)
+    ref_flat, _ = oracle.pack_canonical(sym, bits, specs, [2 * tokens, H, C], [0, 1, 2, -1])
+
+    lay = kv_symbol_layout(tokens, H, C, bits, specs)
+    cache_gpu = _gpu_u8(cache, cuda_device)
+    ids_gpu = native_gpu.block_ids_tensor(ids, cuda_device)
+    flat = native_gpu.pack_from_kv_cache(cache_gpu, ids_gpu, tokens, lay)
+    assert np.array_equal(flat.cpu().numpy(), ref_flat)
+
+
+def test_irregular_plan_restore_falls_back_and_matches(cuda_device):
+    rng = np.random.default_rng(5)
+    tokens, H, C, bs = 300, 2, 32, 16
+    specs = bitref.random_specs(rng, 2 * tokens, H, C, partition=True)  # token-split boxes
+    value = rng.integers(0, 256, (2, tokens, H, C), dtype=np.uint8)
+    flat, offs = oracle.pack_canonical(value.reshape(-1), 6, specs, [2 * tokens, H, C],
+                                       [0, 1, 2, -1])
+    ids, cache = _kv_case(rng, tokens, H, C, bs, False)
+    expect = cache.copy()
+    oracle.restore_layer(flat, offs, 6, specs, tokens, H, C, ids, expect, False)
+    cache_gpu = _gpu_u8(cache, cuda_device)
+    lay = kv_symbol_layout(tokens, H, C, 6, specs)
+    native_gpu.unpack_to_kv_cache(_gpu_u8(flat, cuda_device), lay, tokens, cache_gpu,
+                                  native_gpu.block_ids_tensor(ids, cuda_device))
+    assert np.array_equal(cache_gpu.cpu().numpy(), expect)
+
+
+@pytest.mark.parametrize("blocks_first", [False, True])
+def test_block_scatter_and_gather_match_oracle(cuda_device, blocks_first):
+    rng = np.random.default_rng(11)
+    tokens, H, C, bs = 1234, 8, 256, 16
+    value = rng.integers(0, 256, (2, tokens, H, C), dtype=np.uint8)
+    ids, cache = _kv_case(rng, tokens, H, C, bs, blocks_first)
+    expect = cache.copy()
+    oracle.scatter_kv_cache(value, tokens, H, C, ids, expect, blocks_first)
+    cache_gpu = _gpu_u8(cache, cuda_device)
+    ids_gpu = native_gpu.block_ids_tensor(ids, cuda_device)
+    native_gpu.scatter_kv_blocks(_gpu_u8(value, cuda_device), tokens, cache_gpu, ids_gpu)
+    assert np.array_equal(cache_gpu.cpu().numpy(), expect)
+    back = native_gpu.gather_kv_blocks(cache_gpu, ids_gpu)
+    assert np.array_equal(back.cpu().numpy(), oracle.gather_kv_cache(expect, ids, blocks_first))
+
+
+def test_typed_bf16_cache_round_trip(cuda_device):
+    """bf16 cache tensors (not uint8 views) go through the same byte path."""
+    torch.manual_seed(0)
+    tokens, H, D, bs = 512, 8, 128, 16
+    nblk = tokens // bs
+    kv = torch.randn(2, nblk, bs, H, D, dtype=torch.bfloat16, device=cuda_device)
+    ids = torch.randperm(nblk + 3)[:nblk]
+    cache = torch.zeros(2, nblk + 3, bs, H, D, dtype=torch.bfloat16, device=cuda_device)
+    cache[:, ids.to(cuda_device)] = kv
+    specs = planner_specs(2 * tokens, H, 2 * D, 1 << 16)
+    lay = kv_symbol_layout(tokens, H, 2 * D, 8, specs)
+    ids_gpu = native_gpu.block_ids_tensor(ids, cuda_device)
+    flat = native_gpu.pack_from_kv_cache(cache, ids_gpu, tokens, lay)
+    # the stream is the byte-plane transpose of the token-major K/V bytes
+    sym = kv.reshape(2 * tokens, H, D).contiguous().view(torch.uint8).cpu().numpy()
+    ref, _ = oracle.pack_canonical(sym.reshape(-1), 8, specs, [2 * tokens, H, 2 * D],
+                                   [0, 1, 2, -1])
+    assert np.array_equal(flat.cpu().numpy(), ref)
+    cache2 = torch.zeros_like(cache)
+    native_gpu.unpack_to_kv_cache(flat, lay, tokens, cache2, ids_gpu)
+    assert torch.equal(cache2.view(torch.int16), cache.view(torch.int16))
+
+
+def test_full_llama3_8b_layer_matches_oracle(cuda_device):
+    """One full Llama-3-8B layer: 32768 tokens, 8 KV heads, bf16 (128 MiB of
+    K/V), 1 MiB chunks, randomly permuted block table; pack and restore are
+    compared whole with the oracle."""
+    tokens, H, C, bs = 32768, 8, 256, 16
+    rng = np.random.default_rng(1)
+    specs = planner_specs(2 * tokens, H, C, 1 << 20)
+    assert specs.shape[0] == 128
+    nblk = tokens // bs
+    NB = nblk + 64
+    ids = rng.permutation(NB)[:nblk].astype(np.int64)
+    cache = torch.randint(0, 256, (2, NB, bs, H, C), dtype=torch.uint8, device=cuda_device)
+    cache_np = cache.cpu().numpy()
+    lay = kv_symbol_layout(tokens, H, C, 8, specs)
+    ids_gpu = native_gpu.block_ids_tensor(ids, cuda_device)
+    flat = native_gpu.pack_from_kv_cache(cache, ids_gpu, tokens, lay)
+    sym = oracle.gather_kv_cache(cache_np, ids)
+    ref_flat, offs = oracle.pack_canonical(sym, 8, specs, [2 * tokens, H, C], [0, 1, 2, -1])
+    assert np.array_equal(flat.cpu().numpy(), ref_flat)
+
+    ids2 = rng.permutation(NB)[:nblk].astype(np.int64)
+    dst = torch.randint(0, 256, (2, NB, bs, H, C), dtype=torch.uint8, device=cuda_device)
+    expect = dst.cpu().numpy()
+    oracle.restore_layer(ref_flat, offs, 8, specs, tokens, H, C, ids2, expect)
+    native_gpu.unpack_to_kv_cache(flat, lay, tokens, dst, native_gpu.block_ids_tensor(ids2, cuda_device))
+    assert np.array_equal(dst.cpu().numpy(), expect)
+
+
+def test_native_cpu_api_round_trip(cuda_device):
+    """native_cpu.pack/unpack_canonical_storage_chunks: the reference's stubs,
+    working here through the GPU and returning CPU tensors."""
+    rng = np.random.default_rng(9)
+    T, H, C = 200, 2, 32
+    specs = planner_specs(T, H, C, 2048).tolist()
+    sym = torch.from_numpy(rng.integers(0, 16, T * H * C, dtype=np.uint8))
+    chunks = native_cpu.pack_canonical_storage_chunks(sym, 4, [T, H, C],
+                                                      ["token", "head", "head_dim"], specs)
+    assert all(c.device.type == "cpu" for c in chunks)
+    ref_flat, offs = oracle.pack_canonical(sym.numpy(), 4, specs, [T, H, C], [0, 1, 2, -1])
+    assert [c.numel() for c in chunks] == np.diff(offs).tolist()
+    assert np.array_equal(torch.cat(chunks).numpy(), ref_flat)
+    back = native_cpu.unpack_head_channel_chunks(chunks, 4, T, H, C, specs)
+    assert back.device.type == "cpu" and torch.equal(back, sym)
+
+
+def test_reference_extension_surface(cuda_device):
+    """unpack_canonical_storage_chunks_cuda with the reference's argument list
+    (bitpack_layout_cuda.cpp:316-325)."""
+    rng = np.random.default_rng(4)
+    T, H, C = 64, 2, 16
+    specs = planner_specs(T, H, C, 512)
+    sym = rng.integers(0, 32, T * H * C, dtype=np.uint8)
+    flat, offs = oracle.pack_canonical(sym, 5, specs, [T, H, C], [0, 1, 2, -1])
+    ext = native_gpu.load_bitpack_cuda_extension()
+    out = ext.unpack_canonical_storage_chunks_cuda(
+        _gpu_u8(flat, cuda_device), torch.from_numpy(offs).to(cuda_device),
+        torch.full((specs.shape[0],), 5, dtype=torch.int64, device=cuda_device),
+        torch.tensor([T, H, C]), torch.tensor([0, 1, 2, -1]), T, H, C,
+        torch.from_numpy(specs).to(cuda_device))
+    assert np.array_equal(out.cpu().numpy(), sym)
+    with pytest.raises(RuntimeError, match="byte size mismatch"):
+        bad = offs.copy()
+        bad[1:] += 1
+        ext.unpack_canonical_storage_chunks_cuda(
+            _gpu_u8(np.zeros(bad[-1], np.uint8), cuda_device), torch.from_numpy(bad),
+            torch.full((specs.shape[0],), 5, dtype=torch.int64), torch.tensor([T, H, C]),
+            torch.tensor([0, 1, 2, -1]), T, H, C, torch.from_numpy(specs))
+
+
+def test_errors_raise_with_reference_messages(cuda_device):
+    with pytest.raises(RuntimeError, match="1..8 bit"):
+        native_gpu.unpack_canonical_storage_chunks(
+            [torch.zeros(8, dtype=torch.uint8)], 9, [8, 1, 1], ["token", "head", "head_dim"],
+            [[0, 1, 0, 1, 0, 8]], device=cuda_device)
+    cache = torch.zeros(2, 4, 16, 1, 16, dtype=torch.uint8, device=cuda_device)
+    with pytest.raises(RuntimeError, match="block id out of range"):
+        native_gpu.block_ids_tensor([4], cuda_device, 4)
+    lay = kv_symbol_layout(100, 1, 16, 8, [[0, 1, 0, 16, 0, 200]])
+    with pytest.raises(RuntimeError, match="tokens exceed destination block capacity"):
+        native_gpu.unpack_to_kv_cache(torch.zeros(3200, dtype=torch.uint8, device=cuda_device),
+                                      lay, 100, cache,
+                                      native_gpu.block_ids_tensor([0, 1], cuda_device))
