@@ -313,13 +313,23 @@ int get_plan(const int64_t* offsets, const int64_t* bits, const int64_t* specs,
 // Device helpers
 // ---------------------------------------------------------------------------
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;  // wave tiles per workgroup (along tokens)
+constexpr int kThreads = 256;          // generic and block-copy kernels
+
+// Rows kernels: a lane owns 16 channels x 16 tokens; a wave tile is 8 lanes
+// along channels x 8 lanes along tokens (128 channels x 128 tokens); a
+// workgroup is 16 wave tiles arranged wq x (16 / wq), wq <= 4, i.e. up to
+// 512 channels x 512 tokens.  Large tiles keep both the plane runs read and the
+// row segments written long (512 B at wq = 4), which is what HBM rewards.
+constexpr int kRowsWaves = 16;
+constexpr int kRowsThreads = kRowsWaves * 64;
 constexpr int kSegTokens = 16;         // tokens per lane
 constexpr int kLaneSegs = 8;           // lanes along tokens in a wave tile
 constexpr int kLaneGroups = 8;         // lanes along 16-channel groups
-constexpr int kTilePlanes = kLaneGroups * 16;  // planes per wave tile (128)
-constexpr int kTileTokens = kWaves * kLaneSegs * kSegTokens;  // per workgroup (512)
+constexpr int kWavePlanes = kLaneGroups * 16;  // channels per wave tile (128)
+constexpr int kMaxWq = 4;
+constexpr int kTilePlanes = kMaxWq * kWavePlanes;  // descriptor slots per workgroup
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 struct RowsParams {
   uint8_t* stream;           // 4-byte aligned base of the flat stream
@@ -339,8 +349,10 @@ struct RowsParams {
   int64_t half_stride;       // rows per half step
   int32_t H;
   int32_t nq;                // C / 16
-  int32_t nqg;               // ceil(nq / 8)
-  int32_t nsg_wg;            // workgroups along tokens
+  int32_t wq;                // wave tiles along channels per workgroup (1, 2, 4)
+  int32_t ws;                // wave tiles along tokens per workgroup (16 / wq)
+  int32_t nqt;               // workgroups along channels
+  int32_t nst;               // workgroups along tokens
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -434,7 +446,8 @@ __device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
                                                uint32_t (&out)[4]) {
   if constexpr (ALIGNED) {
     static_assert(BITS == 8, "aligned loads are for 8-bit symbols");
-    const uint4 x = *reinterpret_cast<const uint4*>(p.stream + (P >> 3));
+    // the stream is read once: non-temporal
+    const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.stream + (P >> 3)));
     out[0] = x.x;
     out[1] = x.y;
     out[2] = x.z;
@@ -458,7 +471,8 @@ __device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
 template <bool ALIGNED>
 __device__ __forceinline__ void store_stream(uint8_t* dst, const uint32_t* u, int nbytes) {
   if constexpr (ALIGNED) {
-    *reinterpret_cast<uint4*>(dst) = make_uint4(u[0], u[1], u[2], u[3]);
+    const u32x4 x = {u[0], u[1], u[2], u[3]};
+    __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dst));
   } else {
     int b = 0;
     if ((reinterpret_cast<uintptr_t>(dst) & 3) == 0) {
@@ -469,31 +483,34 @@ __device__ __forceinline__ void store_stream(uint8_t* dst, const uint32_t* u, in
 }
 
 struct TileCoord {
-  int h, half, ql, q;
+  int h, half, slot, q;  // slot: this lane's descriptor group in the workgroup
   int64_t t0;
 };
 
+// Workgroup order: token tiles fastest, then channel tiles, heads, halves.
 __device__ __forceinline__ TileCoord tile_coord(const RowsParams& p) {
   int64_t bid = blockIdx.x;
-  const int sgw = static_cast<int>(bid % p.nsg_wg);
-  bid /= p.nsg_wg;
-  const int qg = static_cast<int>(bid % p.nqg);
-  bid /= p.nqg;
+  const int st = static_cast<int>(bid % p.nst);
+  bid /= p.nst;
+  const int qt = static_cast<int>(bid % p.nqt);
+  bid /= p.nqt;
   TileCoord tc;
   tc.h = static_cast<int>(bid % p.H);
   tc.half = static_cast<int>(bid / p.H);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  tc.ql = lane >> 3;
-  tc.q = qg * kLaneGroups + tc.ql;
-  tc.t0 = (static_cast<int64_t>(sgw * kWaves + wave) * kLaneSegs + (lane & 7)) * kSegTokens;
+  const int wqi = wave % p.wq, wsi = wave / p.wq;
+  tc.slot = wqi * kLaneGroups + (lane >> 3);
+  tc.q = qt * p.wq * kLaneGroups + tc.slot;
+  tc.t0 = (static_cast<int64_t>(st * p.ws + wsi) * kLaneSegs + (lane & 7)) * kSegTokens;
   return tc;
 }
 
 __device__ __forceinline__ void load_descriptors(const RowsParams& p, int64_t* desc) {
-  const int qg = static_cast<int>((blockIdx.x / p.nsg_wg) % p.nqg);
-  const int h = static_cast<int>((blockIdx.x / p.nsg_wg / p.nqg) % p.H);
-  if (threadIdx.x < kTilePlanes) {
-    const int64_t c = static_cast<int64_t>(qg) * kTilePlanes + threadIdx.x;
+  const int qt = static_cast<int>((blockIdx.x / p.nst) % p.nqt);
+  const int h = static_cast<int>((blockIdx.x / p.nst / p.nqt) % p.H);
+  const int n = p.wq * kWavePlanes;
+  if (static_cast<int>(threadIdx.x) < n) {
+    const int64_t c = static_cast<int64_t>(qt) * n + threadIdx.x;
     desc[threadIdx.x] = c < p.C ? p.planes[static_cast<int64_t>(h) * p.C + c] : -1;
   }
   __syncthreads();
@@ -538,7 +555,7 @@ __device__ __forceinline__ int64_t cursor_row(const RowsParams& p, int half, con
 // ---------------------------------------------------------------------------
 
 template <int BITS, bool ALIGNED>
-__global__ __launch_bounds__(kThreads) void rows_unpack_kernel(RowsParams p) {
+__global__ __launch_bounds__(kRowsThreads) void rows_unpack_kernel(RowsParams p) {
   __shared__ int64_t desc[kTilePlanes];
   load_descriptors(p, desc);
   const TileCoord tc = tile_coord(p);
@@ -549,7 +566,7 @@ __global__ __launch_bounds__(kThreads) void rows_unpack_kernel(RowsParams p) {
   uint32_t v[16][4];
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
-    const int64_t d = desc[tc.ql * 16 + k];
+    const int64_t d = desc[tc.slot * 16 + k];
     if (d < 0 || nv <= 0) {
       v[k][0] = v[k][1] = v[k][2] = v[k][3] = 0;
     } else {
@@ -579,15 +596,17 @@ __global__ __launch_bounds__(kThreads) void rows_unpack_kernel(RowsParams p) {
     if (j < nrows) {
       if (j > 0) cursor_next(p, rc);
       const int64_t row = cursor_row(p, tc.half, rc);
-      if (row >= 0)
-        *reinterpret_cast<uint4*>(col + row * p.row_pitch) =
-            make_uint4(o[j][0], o[j][1], o[j][2], o[j][3]);
+      if (row >= 0) {
+        // each row is written once: non-temporal
+        const u32x4 x = {o[j][0], o[j][1], o[j][2], o[j][3]};
+        __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(col + row * p.row_pitch));
+      }
     }
   }
 }
 
 template <int BITS, bool ALIGNED>
-__global__ __launch_bounds__(kThreads) void rows_pack_kernel(RowsParams p) {
+__global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
   __shared__ int64_t desc[kTilePlanes];
   load_descriptors(p, desc);
   const TileCoord tc = tile_coord(p);
@@ -605,7 +624,8 @@ __global__ __launch_bounds__(kThreads) void rows_pack_kernel(RowsParams p) {
       if (j > 0) cursor_next(p, rc);
       const int64_t row = cursor_row(p, tc.half, rc);
       if (row >= 0) {
-        const uint4 x = *reinterpret_cast<const uint4*>(col + row * p.row_pitch);
+        const u32x4 x =
+            __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(col + row * p.row_pitch));
         r[j][0] = x.x;
         r[j][1] = x.y;
         r[j][2] = x.z;
@@ -621,7 +641,7 @@ __global__ __launch_bounds__(kThreads) void rows_pack_kernel(RowsParams p) {
   const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
-    const int64_t d = desc[tc.ql * 16 + k];
+    const int64_t d = desc[tc.slot * 16 + k];
     if (d < 0) continue;
     const int64_t P = d + p.bit_bias + sym0 * BITS;  // byte aligned by plan
     uint32_t u[NU > 4 ? NU : 4];
@@ -810,21 +830,32 @@ void set_stream(RowsParams& p, const uint8_t* flat, int64_t flat_bytes) {
   p.stream_bytes = flat_bytes + static_cast<int64_t>(addr - base);
 }
 
-void set_grid_dims(RowsParams& p, int64_t nhalf, int64_t H, int64_t C, int64_t tile_tokens_total) {
+// Grid of the rows kernels.  When heads are contiguous inside a row
+// (head_pitch == C) and the plane table is indexed h * C + c, the heads are
+// folded into one row of H * C channels so a workgroup can span them.
+void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_total) {
+  if (H > 1 && p.head_pitch == C) {
+    C *= H;
+    H = 1;
+  }
   p.H = static_cast<int32_t>(H);
   p.C = C;
   p.nq = static_cast<int32_t>(C / 16);
-  p.nqg = (p.nq + kLaneGroups - 1) / kLaneGroups;
-  p.nsg_wg = static_cast<int32_t>((tile_tokens_total + kTileTokens - 1) / kTileTokens);
-  (void)nhalf;
+  const int nqg = (p.nq + kLaneGroups - 1) / kLaneGroups;
+  p.wq = nqg >= 4 ? 4 : (nqg >= 2 ? 2 : 1);
+  p.ws = kRowsWaves / p.wq;
+  p.nqt = (nqg + p.wq - 1) / p.wq;
+  const int64_t segs = (tile_tokens_total + kSegTokens - 1) / kSegTokens;
+  const int64_t segs_per_wg = static_cast<int64_t>(p.ws) * kLaneSegs;
+  p.nst = static_cast<int32_t>((segs + segs_per_wg - 1) / segs_per_wg);
 }
 
 int launch_rows(bool pack, const RowsParams& p, int64_t nhalf, int bits, bool aligned,
                 hipStream_t stream) {
-  const int64_t blocks = nhalf * p.H * p.nqg * static_cast<int64_t>(p.nsg_wg);
+  const int64_t blocks = nhalf * p.H * static_cast<int64_t>(p.nqt) * p.nst;
   if (blocks <= 0) return ORIGAMI_OK;
   if (blocks > INT32_MAX) return fail(ORIGAMI_ERR_INVALID, "layer too large for one launch");
-  const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kRowsThreads);
 #define ORIGAMI_ROWS_CASE(B)                                                           \
   case B:                                                                              \
     if (pack) {                                                                        \
@@ -954,7 +985,7 @@ int origami_unpack_canonical_storage_chunks(
     p.bs = T;
     p.blk_stride = 0;
     p.half_stride = 0;
-    set_grid_dims(p, 1, H, C, T);
+    set_grid_dims(p, H, C, T);
     const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks);
     return launch_rows(false, p, 1, plan->info.bits, al, stream);
   }
@@ -1004,7 +1035,7 @@ int origami_pack_canonical_storage_chunks(
     p.row_pitch = st.token;
     p.head_pitch = st.head;
     p.bs = T;
-    set_grid_dims(p, 1, H, C, T);
+    set_grid_dims(p, H, C, T);
     const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks) && T % 16 == 0;
     return launch_rows(true, p, 1, plan->info.bits, al, stream);
   }
@@ -1062,7 +1093,7 @@ int origami_unpack_canonical_to_kv_cache(
   p.bs = block_size;
   p.blk_stride = blk_stride;
   p.half_stride = half_stride;
-  set_grid_dims(p, 2, num_heads, head_bytes, p.row_tokens);
+  set_grid_dims(p, num_heads, head_bytes, p.row_tokens);
   const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks) &&
                   tokens % 16 == 0;
   return launch_rows(false, p, 2, plan->info.bits, al, stream);
@@ -1112,7 +1143,7 @@ int origami_pack_canonical_from_kv_cache(
   p.bs = block_size;
   p.blk_stride = blk_stride;
   p.half_stride = half_stride;
-  set_grid_dims(p, 2, num_heads, head_bytes, tokens);
+  set_grid_dims(p, num_heads, head_bytes, tokens);
   const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks) &&
                   tokens % 16 == 0;
   return launch_rows(true, p, 2, plan->info.bits, al, stream);

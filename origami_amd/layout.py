@@ -154,7 +154,8 @@ def _make_cached(shape: tuple[int, ...], layout: tuple[str, ...], bits: tuple[in
     specs = np.frombuffer(spec_bytes, dtype=np.int64).reshape(n, 6).copy()
     bits_arr = np.asarray(bits, dtype=np.int64).reshape(n)
     if n and (bits_arr.min() < 1 or bits_arr.max() > 8):
-        raise ValueError("origami_bits must be in the range 1..8")
+        # the reference raises this from its extension (bitpack_layout_cuda.cpp:58-61)
+        raise RuntimeError("Origami CUDA bitpack supports only 1..8 bit symbols")
     sizes = (chunk_symbol_counts(specs) * bits_arr + 7) // 8
     offsets = np.zeros(n + 1, dtype=np.int64)
     offsets[1:] = np.cumsum(sizes)
