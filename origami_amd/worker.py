@@ -1,0 +1,456 @@
+"""Connector worker: layer-wise restore and save of KV through the HIP layout path.
+
+Mirrors OrigamiConnectorWorker (vllm/.../origami/worker.py).  The public
+methods and their semantics are the reference's:
+
+* start_load_kv (worker.py:426-481): one future per (request, layer); the
+  request's restore runs on a worker thread.
+* wait_for_layer_load (:553-572): waits for the layer's futures, then makes
+  the current (attention) stream wait on the layer's completion event.
+* save_kv_layer / wait_for_save (:619-663): per (save request, layer) pack and
+  compress, then store.put per cache key.
+* get_finished (:2441-2496): request ids whose restore completed; failures
+  are re-raised.
+
+What changes is the data path.  A layer saved with the raw_byte_planes
+adapter is packed on the GPU straight from the paged cache (fused block gather
++ plane-major pack) and restored through LayerRestorePipeline: decompression
+into pinned staging, H2D on a copy stream, fused unpack + block-table scatter on
+a compute stream, one event per layer.  Payloads in the reference's raw_bytes
+format restore through the same pipeline with a block scatter.  Other
+canonical payloads unpack on the GPU and go through copy_kv_to_hbm.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import time
+from concurrent.futures import Future, ThreadPoolExecutor
+from dataclasses import dataclass
+from pathlib import Path
+from threading import Lock
+from typing import Any
+
+import torch
+
+from origami_amd.benchmark_utils import copy_kv_to_hbm, nvtx_range, write_jsonl
+from origami_amd.config import OrigamiConfig
+from origami_amd.layout import STORAGE_LAYOUT, CanonicalLayout, canonical_axis_sizes
+from origami_amd.lossless import native_gpu
+from origami_amd.lossless.chunking import PlannedChunk, plan_head_channel_chunks
+from origami_amd.lossless.cpu_qat import CpuLosslessCodec
+from origami_amd.metadata import (
+    ChunkLayout,
+    ChunkRecord,
+    LayerPayload,
+    OrigamiConnectorMetadata,
+    OrigamiPayload,
+    OrigamiRestoreRequest,
+    OrigamiSaveRequest,
+)
+from origami_amd.quantization import QuantizerAdapter, create_quantizer_adapter
+from origami_amd.quantization.raw_tensor import RawBytePlanesAdapter
+from origami_amd.restore_pipeline import LayerRestorePipeline
+from origami_amd.store import OrigamiStore
+
+_NATIVE_LAYOUT_KEY = "origami_native_layout"
+
+
+def _layer_index(layer_name: str) -> int:
+    """Trailing integer of a layer name (worker.py:63-71)."""
+    digits = ""
+    for ch in reversed(layer_name):
+        if ch.isdigit():
+            digits = ch + digits
+        elif digits:
+            break
+    return int(digits) if digits else 0
+
+
+def _config_hash(config: dict[str, Any]) -> str:
+    return hashlib.sha256(json.dumps(config, sort_keys=True, default=str).encode()).hexdigest()
+
+
+@dataclass
+class _LayerLoadResult:
+    event: torch.cuda.Event | None = None
+    pending_metrics: list | None = None
+    wait_on_current_stream: bool = True
+
+
+def _layout_to_spec(layout: ChunkLayout) -> list[int]:
+    return [int(layout.head_start), int(layout.head_end), int(layout.channel_start),
+            int(layout.channel_end), int(layout.token_start), int(layout.token_end)]
+
+
+class OrigamiConnectorWorker:
+
+    def __init__(self, config: OrigamiConfig, store: OrigamiStore,
+                 kv_cache_config: Any | None = None, *, fused_attention_enabled: bool = False):
+        self.config = config
+        self.store = store
+        self.kv_cache_config = kv_cache_config
+        if fused_attention_enabled and config.fused_attention == "required":
+            raise RuntimeError("Origami fused attention is outside this build")
+        self.fused_attention_enabled = False
+        self.quantizer: QuantizerAdapter = create_quantizer_adapter(
+            config.quantizer, config.quantizer_config)
+        self.cpu_codec = CpuLosslessCodec(backend=config.lossless_cpu_backend,
+                                          allow_zlib_fallback=config.allow_zlib_fallback)
+        self.kv_caches: dict[str, torch.Tensor] = {}
+        self.layer_to_cache_group: dict[str, int] = {}
+        self._executor = ThreadPoolExecutor(max_workers=max(1, config.qat_threads))
+        self._pending_layer_futures: dict[str, list[Future]] = {}
+        self._pending_request_layer_futures: dict[str, list[Future]] = {}
+        self._restore_futures: list[Future] = []
+        self._restore_future_to_request_id: dict[Future, str] = {}
+        self._save_futures: list[Future] = []
+        self._save_payloads: dict[str, OrigamiPayload] = {}
+        self._save_lock = Lock()
+        self._pipeline_lock = Lock()
+        self._pipelines: dict[int, LayerRestorePipeline] = {}
+        self._metadata: OrigamiConnectorMetadata | None = None
+        self.metrics_path = (str(Path(config.metrics_dir) / "origami_metrics.jsonl")
+                             if config.metrics_dir else None)
+        if config.bitunpack_device in {"gpu", "cuda", "hip"} and not native_gpu.available():
+            raise RuntimeError("Origami GPU bitunpack requested but the HIP layout library "
+                               "or a ROCm device is unavailable")
+
+    # ------------------------------------------------------------------ setup
+
+    def register_kv_caches(self, kv_caches: dict[str, torch.Tensor]) -> None:
+        self.kv_caches = dict(kv_caches)
+        mapping: dict[str, int] = {}
+        for idx, group in enumerate(getattr(self.kv_cache_config, "kv_cache_groups", None) or []):
+            for name in getattr(group, "layer_names", ()):
+                mapping[str(name)] = idx
+        for name in self.kv_caches:
+            mapping.setdefault(name, 0)
+        self.layer_to_cache_group = mapping
+
+    def _pipeline(self, device: torch.device, slot_bytes: int) -> LayerRestorePipeline:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        with self._pipeline_lock:
+            pipe = self._pipelines.get(index)
+            if pipe is None or pipe.slot_bytes < slot_bytes:
+                if pipe is not None:
+                    pipe.synchronize()
+                pipe = LayerRestorePipeline(torch.device("cuda", index), slot_bytes,
+                                            num_slots=self.config.restore_slots)
+                self._pipelines[index] = pipe
+            return pipe
+
+    # --------------------------------------------------------------- restore
+
+    def start_load_kv(self, metadata: OrigamiConnectorMetadata) -> None:
+        self._metadata = metadata
+        if not metadata.reqs_to_restore:
+            return
+        restores = list(metadata.reqs_to_restore.values())
+        write_jsonl(self.metrics_path, {
+            "type": "restore_batch_meta", "system": "origami", "restore_count": len(restores),
+            "request_ids": [r.request_id for r in restores],
+            "cache_keys": [r.cache_key for r in restores], "ts": time.time()})
+        for restore in restores:
+            layer_futures: dict[str, Future] = {}
+            for layer_name in self.kv_caches:
+                fut: Future = Future()
+                layer_futures[layer_name] = fut
+                self._pending_layer_futures.setdefault(layer_name, []).append(fut)
+            self._pending_request_layer_futures[restore.request_id] = list(layer_futures.values())
+            rf = self._executor.submit(self._restore_request_layer_futures, restore,
+                                       layer_futures)
+            self._restore_futures.append(rf)
+            self._restore_future_to_request_id[rf] = restore.request_id
+
+    def _restore_request_layer_futures(self, restore: OrigamiRestoreRequest,
+                                       layer_futures: dict[str, Future]) -> str:
+        try:
+            payload = self.store.prepare_for_restore(restore.cache_key)
+            # layers are issued in model order (the kv_caches order)
+            for layer_name, fut in layer_futures.items():
+                if fut.done():
+                    continue
+                try:
+                    result = self._restore_layer(restore, payload, layer_name)
+                except Exception as exc:  # noqa: BLE001 - delivered through the future
+                    fut.set_exception(exc)
+                else:
+                    fut.set_result(result)
+            return restore.request_id
+        except Exception as exc:
+            for fut in layer_futures.values():
+                if not fut.done():
+                    fut.set_exception(exc)
+            raise
+
+    def _restore_layer(self, restore: OrigamiRestoreRequest, payload: OrigamiPayload,
+                       layer_name: str) -> _LayerLoadResult | None:
+        layer_payload = payload.layer_payloads.get(layer_name)
+        if layer_payload is None or layer_name not in self.kv_caches:
+            return None
+        kv_cache = self.kv_caches[layer_name]
+        group = self.layer_to_cache_group.get(layer_name, 0)
+        if group >= len(restore.block_ids_per_group):
+            return None
+        block_ids = list(restore.block_ids_per_group[group])
+        if not block_ids:
+            return None
+        meta = layer_payload.quant_metadata
+        native = meta.get(_NATIVE_LAYOUT_KEY) or {}
+        fmt = str(meta.get("format", layer_payload.quantizer))
+        if not native or int(native.get("version", 0)) != 2:
+            raise RuntimeError(f"Origami layer {layer_name!r}: unsupported native layout "
+                               f"metadata version {native.get('version')!r}")
+        layout = CanonicalLayout.make(native["source_shape"], native["source_layout"],
+                                      int(native["bits"]), native.get("chunk_specs", []))
+        if len(layer_payload.chunks) != layout.num_chunks:
+            raise RuntimeError("Origami native layout metadata chunk count does not match "
+                               "payload chunks")
+        _, nb, bs, H, head_bytes = native_gpu.cache_geometry(kv_cache)
+        with nvtx_range("origami:restore_layer"):
+            if fmt == "raw_byte_planes" and kv_cache.is_cuda:
+                return self._restore_byte_planes(layer_payload, layout, kv_cache, block_ids, bs,
+                                                 nb, meta)
+            if fmt == "raw_bytes" and kv_cache.is_cuda and self._raw_bytes_scatterable(
+                    meta, kv_cache, layout):
+                return self._restore_raw_bytes(layer_payload, layout, kv_cache, block_ids, nb, meta)
+            return self._restore_generic(restore, layer_payload, layout, kv_cache, block_ids)
+
+    def _fill_from_chunks(self, layer_payload: LayerPayload, layout: CanonicalLayout):
+        sizes = layout.chunk_sizes()
+        for rec, size in zip(layer_payload.chunks, sizes):
+            if int(rec.unpacked_bytes) != size:
+                raise RuntimeError("Origami CUDA packed chunk byte size mismatch")
+
+        def fill(staging: torch.Tensor) -> None:
+            off = layout.offsets
+            outs = [staging[int(off[k]):int(off[k + 1])] for k in range(layout.num_chunks)]
+            self.cpu_codec.decompress_into([r.compressed for r in layer_payload.chunks], outs)
+        return fill
+
+    def _restore_byte_planes(self, layer_payload, layout, kv_cache, block_ids, bs, nb, meta):
+        tokens = int(meta.get("token_count", layout.token_count // 2))
+        if layout.token_count != 2 * tokens:
+            raise RuntimeError("raw_byte_planes symbol token axis must be 2 * token_count")
+        needed = -(-tokens // bs)
+        if len(block_ids) < needed:
+            raise RuntimeError("tokens exceed destination block capacity")
+        pipe = self._pipeline(kv_cache.device, layout.stream_bytes)
+        ids_dev = native_gpu.block_ids_tensor(block_ids[:needed], kv_cache.device, nb)
+        ids_dev.record_stream(pipe.compute_stream)
+        event = pipe.submit(
+            self._fill_from_chunks(layer_payload, layout), layout.stream_bytes,
+            lambda flat: native_gpu.unpack_to_kv_cache(flat, layout, tokens, kv_cache, ids_dev))
+        return _LayerLoadResult(event=event)
+
+    @staticmethod
+    def _raw_bytes_scatterable(meta, kv_cache, layout) -> bool:
+        shape = [int(d) for d in meta.get("shape", [])]
+        dtype = str(meta.get("dtype", ""))
+        return (len(shape) == 5 and shape[0] == 2 and tuple(shape[2:]) == tuple(kv_cache.shape[2:])
+                and dtype == str(kv_cache.dtype).replace("torch.", "")
+                and layout.shape[0] == 1 and layout.shape[1] == 1 and layout.uniform_bits == 8)
+
+    def _restore_raw_bytes(self, layer_payload, layout, kv_cache, block_ids, nb, meta):
+        """Reference raw_bytes payload ([1, 1, N] bits 8 = the blocks' bytes in
+        [2, nblk, bs, H, D] order): H2D + block scatter."""
+        nblk = int(meta["shape"][1])
+        if len(block_ids) < nblk:
+            raise RuntimeError("tokens exceed destination block capacity")
+        tokens = nblk * int(kv_cache.shape[2])
+        pipe = self._pipeline(kv_cache.device, layout.stream_bytes)
+        ids_dev = native_gpu.block_ids_tensor(block_ids[:nblk], kv_cache.device, nb)
+        ids_dev.record_stream(pipe.compute_stream)
+        event = pipe.submit(
+            self._fill_from_chunks(layer_payload, layout), layout.stream_bytes,
+            lambda flat: native_gpu.scatter_kv_blocks(flat, tokens, kv_cache, ids_dev))
+        return _LayerLoadResult(event=event)
+
+    def _restore_generic(self, restore, layer_payload, layout, kv_cache, block_ids):
+        chunks = self.cpu_codec.decompress_many([r.compressed for r in layer_payload.chunks],
+                                                layout.chunk_sizes())
+        device = kv_cache.device
+        symbols = native_gpu.unpack_canonical_storage_chunks(
+            chunks, [int(b) for b in layout.bits], layout.shape, layout.layout, layout.specs,
+            device=device)
+        native = layer_payload.quant_metadata.get(_NATIVE_LAYOUT_KEY) or {}
+        count = int(native.get("symbol_count", symbols.numel()))
+        kv = self.quantizer.dequantize(symbols.reshape(-1)[:count],
+                                       layer_payload.quant_metadata)
+        _, event = copy_kv_to_hbm(kv_cache=kv_cache, block_ids=block_ids, value=kv,
+                                  request_id=restore.metric_request_id or restore.request_id,
+                                  cache_key=restore.cache_key, system="origami",
+                                  layer_name=layer_payload.layer_name,
+                                  metrics_path=self.metrics_path, synchronize=False,
+                                  return_event=True)
+        return _LayerLoadResult(event=event)
+
+    def wait_for_layer_load(self, layer_name: str) -> None:
+        for fut in self._pending_layer_futures.pop(layer_name, []):
+            result = fut.result()
+            event = result.event if isinstance(result, _LayerLoadResult) else result
+            wait = not isinstance(result, _LayerLoadResult) or result.wait_on_current_stream
+            if event is not None and wait and torch.cuda.is_available():
+                torch.cuda.current_stream().wait_event(event)
+
+    # ------------------------------------------------------------------ save
+
+    def save_kv_layer(self, layer_name: str, kv_layer: torch.Tensor, attn_metadata: Any) -> None:
+        del attn_metadata
+        if self._metadata is None or not self._metadata.reqs_to_save:
+            return
+        for save in self._metadata.reqs_to_save.values():
+            group = self.layer_to_cache_group.get(layer_name, 0)
+            if group >= len(save.block_ids_per_group):
+                continue
+            block_ids = save.block_ids_per_group[group]
+            if not block_ids:
+                continue
+            if isinstance(self.quantizer, RawBytePlanesAdapter) and kv_layer.is_cuda:
+                fut = self._save_byte_planes(save, layer_name, kv_layer, tuple(block_ids))
+            else:
+                fut = self._save_generic(save, layer_name, kv_layer, tuple(block_ids))
+            self._save_futures.append(fut)
+
+    def _plan(self, layer_name: str, token_count: int, heads: int, head_bytes: int
+              ) -> list[PlannedChunk]:
+        return plan_head_channel_chunks(
+            layer_index=_layer_index(layer_name), num_heads=heads, head_dim=head_bytes,
+            token_count=token_count, bytes_per_symbol=1,
+            min_bytes=self.config.chunk_min_bytes, target_bytes=self.config.chunk_target_bytes,
+            max_bytes=self.config.chunk_max_bytes)
+
+    def _native_metadata(self, bits, shape, layout_names, specs, symbol_count) -> dict:
+        T, H, C, _, _ = canonical_axis_sizes(shape, layout_names)
+        return {
+            "version": 2, "bits": int(bits), "source_shape": [int(d) for d in shape],
+            "source_layout": list(layout_names), "storage_layout": STORAGE_LAYOUT,
+            "token_count": T, "num_heads": H, "head_dim": C, "symbol_count": int(symbol_count),
+            "layout_policy": self.config.layout_policy, "bitpack": bool(self.config.bitpack),
+            "chunk_specs": [list(map(int, s)) for s in specs],
+        }
+
+    def _save_byte_planes(self, save: OrigamiSaveRequest, layer_name: str, kv_layer, block_ids):
+        """Fused GPU gather + pack from the paged cache, on the current stream
+        (so it follows the model's writes of this layer), then D2H into
+        pinned memory; compression runs on a worker thread."""
+        _, nb, bs, H, head_bytes = native_gpu.cache_geometry(kv_layer)
+        tokens = len(block_ids) * bs  # whole saved blocks (worker.py:1881-1897)
+        planned = self._plan(layer_name, 2 * tokens, H, head_bytes)
+        specs = [_layout_to_spec(p.layout) for p in planned]
+        layout = CanonicalLayout.make([2 * tokens, H, head_bytes], ["token", "head", "head_dim"],
+                                      8, specs)
+        ids_dev = native_gpu.block_ids_tensor(list(block_ids), kv_layer.device, nb)
+        flat = native_gpu.pack_from_kv_cache(kv_layer, ids_dev, tokens, layout)
+        host = torch.empty(layout.stream_bytes, dtype=torch.uint8, pin_memory=True)
+        host.copy_(flat, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+        meta = RawBytePlanesAdapter.metadata_for(kv_layer.dtype, tokens, H,
+                                                 int(kv_layer.shape[4]))
+        meta[_NATIVE_LAYOUT_KEY] = self._native_metadata(8, layout.shape, list(layout.layout),
+                                                         specs, layout.symbol_count)
+
+        def finish():
+            done.synchronize()  # pack and D2H (current stream) have completed
+            off = layout.offsets
+            raw = [host[int(off[k]):int(off[k + 1])] for k in range(layout.num_chunks)]
+            return save, self._layer_payload(save, layer_name, planned, raw, meta)
+        return self._executor.submit(finish)
+
+    def _save_generic(self, save: OrigamiSaveRequest, layer_name: str, kv_layer, block_ids):
+        """Adapter path: gather the blocks, quantize, pack on the GPU, compress."""
+        if kv_layer.is_cuda:
+            _, nb, _, _, _ = native_gpu.cache_geometry(kv_layer)
+            ids_dev = native_gpu.block_ids_tensor(list(block_ids), kv_layer.device, nb)
+            dim = 1 if kv_layer.shape[0] in (1, 2) else 0  # _block_dim (worker.py:1881-1885)
+            kv_blocks = torch.index_select(kv_layer, dim, ids_dev)
+        else:
+            dim = 1 if kv_layer.shape[0] in (1, 2) else 0
+            kv_blocks = torch.index_select(kv_layer, dim, torch.tensor(list(block_ids)))
+        quantized = self.quantizer.quantize(kv_blocks, layer_group=layer_name)
+        flat = quantized.symbols.reshape(-1).to(torch.uint8)
+        md = quantized.metadata
+        bits = int(md.get("origami_bits", 8)) if self.config.bitpack else 8
+        T, H, C, shape, names = canonical_axis_sizes(md["origami_symbol_shape"],
+                                                     md["origami_symbol_layout"])
+        planned = self._plan(layer_name, T, H, C)
+        specs = [_layout_to_spec(p.layout) for p in planned]
+        layout = CanonicalLayout.make(shape, names, bits, specs)
+        device = kv_layer.device if kv_layer.is_cuda else torch.device("cuda")
+        stream, _ = native_gpu.pack_canonical_storage_flat(flat.to(device), bits, shape, names,
+                                                           specs)
+        host = stream.cpu()
+        meta = dict(md)
+        meta[_NATIVE_LAYOUT_KEY] = self._native_metadata(bits, shape, names, specs, flat.numel())
+        off = layout.offsets
+        raw = [host[int(off[k]):int(off[k + 1])] for k in range(layout.num_chunks)]
+        return self._executor.submit(lambda: (save, self._layer_payload(save, layer_name,
+                                                                        planned, raw, meta)))
+
+    def _layer_payload(self, save, layer_name, planned, raw, meta) -> LayerPayload:
+        compressed = self.cpu_codec.compress_many(raw)
+        chunks = []
+        for idx, (p, r, c) in enumerate(zip(planned, raw, compressed)):
+            lay = ChunkLayout(
+                layer_index=p.layout.layer_index, head_start=p.layout.head_start,
+                head_end=p.layout.head_end, channel_start=p.layout.channel_start,
+                channel_end=p.layout.channel_end, token_start=save.token_start,
+                token_end=save.token_start + save.num_tokens, unpacked_bytes=int(r.numel()))
+            chunks.append(ChunkRecord(chunk_id=idx, layout=lay, codec=self.cpu_codec.backend,
+                                      compressed=c, compressed_bytes=int(c.numel()),
+                                      unpacked_bytes=int(r.numel())))
+        return LayerPayload(layer_name=layer_name, quantizer=self.quantizer.quantizer_id,
+                            quant_metadata=meta, chunks=chunks)
+
+    def wait_for_save(self) -> None:
+        for fut in self._save_futures:
+            save, layer_payload = fut.result()
+            with self._save_lock:
+                payload = self._save_payloads.get(save.cache_key)
+                if payload is None:
+                    payload = OrigamiPayload(
+                        cache_key=save.cache_key, request_id=save.request_id,
+                        quantizer=self.quantizer.quantizer_id,
+                        quantizer_config_hash=_config_hash(self.config.quantizer_config),
+                        token_start=save.token_start, token_count=save.num_tokens)
+                    self._save_payloads[save.cache_key] = payload
+                payload.layer_payloads[layer_payload.layer_name] = layer_payload
+        for payload in self._save_payloads.values():
+            self.store.put(payload)
+        self._save_futures.clear()
+        self._save_payloads.clear()
+
+    # -------------------------------------------------------------- finished
+
+    def get_finished(self) -> tuple[set[str], set[str]]:
+        finished_recving: set[str] = set()
+        for rf in list(self._restore_futures):
+            if not rf.done():
+                continue
+            req_id = self._restore_future_to_request_id.pop(rf, "")
+            self._restore_futures.remove(rf)
+            if not req_id:
+                continue
+            try:
+                rf.result()
+            except Exception:
+                self._pending_request_layer_futures.pop(req_id, None)
+                for name, futs in self._pending_layer_futures.items():
+                    self._pending_layer_futures[name] = [f for f in futs if not f.done()]
+                raise
+            layer_futs = self._pending_request_layer_futures.get(req_id, [])
+            if layer_futs and all(f.done() for f in layer_futs):
+                try:
+                    for f in layer_futs:
+                        f.result()
+                finally:
+                    self._pending_request_layer_futures.pop(req_id, None)
+                finished_recving.add(req_id)
+        return set(), finished_recving
+
+    def shutdown(self) -> None:
+        self._executor.shutdown(wait=True)
+        for pipe in self._pipelines.values():
+            pipe.synchronize()

@@ -1,0 +1,113 @@
+"""Host-side connector logic (no GPU): configuration, store, codec, value
+normalisation and failure delivery through the restore futures."""
+import types
+
+import pytest
+import torch
+
+from origami_amd.benchmark_utils import normalize_kv_value
+from origami_amd.config import OrigamiConfig
+from origami_amd.connector import KVConnectorRole, OrigamiConnector
+from origami_amd.lossless.cpu_qat import CpuLosslessCodec
+from origami_amd.metadata import OrigamiConnectorMetadata, OrigamiRestoreRequest
+from origami_amd.quantization import create_quantizer_adapter
+from origami_amd.store import InMemoryOrigamiStore, create_origami_store
+
+
+def _vllm_config(extra):
+    return types.SimpleNamespace(kv_transfer_config=types.SimpleNamespace(
+        kv_connector_extra_config=extra))
+
+
+def test_config_reads_reference_keys():
+    cfg = OrigamiConfig.from_vllm_config(_vllm_config({
+        "origami_quantizer": "raw_byte_planes", "origami_chunk_min_bytes": 4096,
+        "origami_chunk_target_bytes": 8192, "origami_chunk_max_bytes": 8192,
+        "origami_lossless_cpu_backend": "zlib", "origami_bitunpack_device": "AUTO",
+        "origami_qat_threads": 4, "origami_unrelated_knob": 1}))
+    assert cfg.quantizer == "raw_byte_planes" and cfg.chunk_target_bytes == 8192
+    assert cfg.bitunpack_device == "auto" and cfg.qat_threads == 4
+    with pytest.raises(ValueError):
+        OrigamiConfig.from_extra_config({"origami_chunk_min_bytes": 10,
+                                         "origami_chunk_target_bytes": 5})
+    with pytest.raises(ValueError):
+        OrigamiConfig.from_extra_config({"origami_layout_policy": "zigzag"})
+
+
+def test_codec_backends():
+    data = torch.randint(0, 4, (100000,), dtype=torch.uint8)
+    for backend in ("zlib", "raw"):
+        codec = CpuLosslessCodec(backend=backend)
+        comp = codec.compress_many([data, data[:10]])
+        out = codec.decompress_many(comp, [100000, 10])
+        assert torch.equal(out[0], data) and torch.equal(out[1], data[:10])
+    assert CpuLosslessCodec(backend="zlib").compress(data).numel() < data.numel() // 2
+    with pytest.raises(RuntimeError, match="QAT backend is not available"):
+        CpuLosslessCodec(backend="qat")
+    assert CpuLosslessCodec(backend="qat", allow_zlib_fallback=True).backend == "zlib"
+    with pytest.raises(RuntimeError, match="decoded"):
+        CpuLosslessCodec(backend="zlib").decompress(CpuLosslessCodec._zlib_compress(data),
+                                                    output_bytes=5)
+
+
+def test_store_round_trip_and_missing_key():
+    store = create_origami_store("memory://t1")
+    assert isinstance(store, InMemoryOrigamiStore)
+    with pytest.raises(KeyError):
+        store.get("nope")
+    with pytest.raises(ValueError):
+        create_origami_store("file:///tmp/x")
+
+
+def test_adapters_byte_views():
+    kv = torch.randn(2, 3, 4, 2, 8, dtype=torch.bfloat16)
+    planes = create_quantizer_adapter("raw_byte_planes")
+    q = planes.quantize(kv)
+    assert q.metadata["origami_symbol_shape"] == [2 * 12, 2, 16]
+    assert torch.equal(q.symbols.view(torch.bfloat16).reshape(2, 12, 2, 8),
+                       kv.reshape(2, 12, 2, 8))
+    back = planes.dequantize(q.symbols, q.metadata)
+    assert torch.equal(back.view(torch.int16), kv.reshape(2, 12, 2, 8).view(torch.int16))
+    raw = create_quantizer_adapter("raw_bytes")
+    r = raw.quantize(kv)
+    assert r.metadata["origami_symbol_shape"] == [1, 1, kv.numel() * 2]
+    assert torch.equal(raw.dequantize(r.symbols, r.metadata).view(torch.int16),
+                       kv.view(torch.int16))
+    with pytest.raises(ValueError):
+        create_quantizer_adapter("cachegen")
+
+
+def test_normalize_kv_value_shapes():
+    cache = torch.zeros(2, 10, 4, 2, 8)
+    tok = torch.randn(2, 10, 2, 8)
+    assert torch.equal(normalize_kv_value(cache, 3, tok), tok)
+    assert torch.equal(normalize_kv_value(cache, 2, tok), tok[:, :8])
+    assert torch.equal(normalize_kv_value(cache, 3, tok.permute(0, 2, 1, 3)), tok)
+    blocks = torch.randn(2, 3, 4, 2, 8)
+    assert torch.equal(normalize_kv_value(cache, 3, blocks), blocks.reshape(2, 12, 2, 8))
+    assert torch.equal(normalize_kv_value(cache, 3, blocks.permute(1, 0, 2, 3, 4)),
+                       blocks.reshape(2, 12, 2, 8))
+    with pytest.raises(ValueError):
+        normalize_kv_value(cache, 3, torch.randn(3, 10, 2, 8))
+
+
+def test_unknown_cache_key_fails_through_futures():
+    """store.get raises KeyError on the worker thread; the layer futures carry
+    it to wait_for_layer_load and get_finished re-raises it."""
+    conn = OrigamiConnector(_vllm_config({"origami_quantizer": "raw_byte_planes",
+                                          "origami_lossless_cpu_backend": "zlib",
+                                          "origami_store_uri": "memory://cpu-fail"}),
+                            KVConnectorRole.WORKER)
+    conn.register_kv_caches({"layers.0.attn": torch.zeros(2, 4, 4, 1, 8),
+                             "layers.1.attn": torch.zeros(2, 4, 4, 1, 8)})
+    md = OrigamiConnectorMetadata(reqs_to_restore={"r1": OrigamiRestoreRequest(
+        request_id="r1", cache_key="missing", block_ids_per_group=((0, 1),), num_tokens=8)})
+    conn.bind_connector_metadata(md)
+    conn.start_load_kv(None)
+    with pytest.raises(KeyError):
+        conn.wait_for_layer_load("layers.0.attn")
+    conn.connector_worker._restore_futures[0].exception()  # wait for the request thread
+    with pytest.raises(KeyError):
+        conn.get_finished(set())
+    with pytest.raises(NotImplementedError):
+        conn.build_connector_meta(None)
