@@ -62,6 +62,16 @@ const char* origami_last_error(void);
 int origami_abi_version(void);
 
 /*
+ * Caps the number of workgroups of the row kernels (the fused restore / save
+ * and the fast unpack / pack paths) launched later on the calling thread;
+ * each workgroup then loops over several tiles.  0 restores the default (one
+ * workgroup per tile).  Returns the previous cap.  New; no reference
+ * counterpart: a restore that runs hidden behind host-to-device copies uses it
+ * to take a smaller share of HBM bandwidth at a time.
+ */
+int64_t origami_set_rows_grid_limit(int64_t max_workgroups);
+
+/*
  * Host-only validation of a canonical chunk layout.  Replaces the checks of
  * read_source_layout / read_chunk_specs / check_bits /
  * packed_bytes_for_symbols and the byte-size loop of

@@ -28,6 +28,7 @@ _p = ctypes.c_void_p
 # name -> argument types (return type is int for all but origami_last_error)
 _SIGNATURES: dict[str, list] = {
     "origami_abi_version": [],
+    "origami_set_rows_grid_limit": [_i64],
     "origami_validate_chunks": [_p, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64],
     "origami_plan_planes": [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "origami_unpack_canonical_storage_chunks": [
@@ -74,6 +75,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(L, name)
                 fn.restype = ctypes.c_int
                 fn.argtypes = args
+            L.origami_set_rows_grid_limit.restype = ctypes.c_int64
             if L.origami_abi_version() != ABI_VERSION:
                 raise RuntimeError("liborigami_layout.so ABI version mismatch; rebuild it")
             _lib = L
@@ -98,3 +100,8 @@ def host_ptr(arr: np.ndarray) -> int:
 
 def i64_array(values) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(values, dtype=np.int64))
+
+
+def set_rows_grid_limit(max_workgroups: int) -> int:
+    """Caps row-kernel workgroups for launches on this thread; returns the old cap."""
+    return int(lib().origami_set_rows_grid_limit(int(max_workgroups)))

@@ -43,6 +43,11 @@ namespace {
 
 thread_local std::string g_last_error;
 
+// Upper bound on the workgroups of one rows-kernel launch on this thread
+// (0: one workgroup per tile).  A restore that runs hidden behind other work
+// can be spread thinner over the GPU with it.
+thread_local int64_t g_rows_grid_limit = 0;
+
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
   return code;
@@ -353,6 +358,7 @@ struct RowsParams {
   int32_t ws;                // wave tiles along tokens per workgroup (16 / wq)
   int32_t nqt;               // workgroups along channels
   int32_t nst;               // workgroups along tokens
+  int64_t ntiles;            // workgroup tiles; a workgroup loops over tiles
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -487,16 +493,15 @@ struct TileCoord {
   int64_t t0;
 };
 
-// Workgroup order: token tiles fastest, then channel tiles, heads, halves.
-__device__ __forceinline__ TileCoord tile_coord(const RowsParams& p) {
-  int64_t bid = blockIdx.x;
-  const int st = static_cast<int>(bid % p.nst);
-  bid /= p.nst;
-  const int qt = static_cast<int>(bid % p.nqt);
-  bid /= p.nqt;
+// Tile order: token tiles fastest, then channel tiles, heads, halves.
+__device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, int64_t tile) {
+  const int st = static_cast<int>(tile % p.nst);
+  tile /= p.nst;
+  const int qt = static_cast<int>(tile % p.nqt);
+  tile /= p.nqt;
   TileCoord tc;
-  tc.h = static_cast<int>(bid % p.H);
-  tc.half = static_cast<int>(bid / p.H);
+  tc.h = static_cast<int>(tile % p.H);
+  tc.half = static_cast<int>(tile / p.H);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wqi = wave % p.wq, wsi = wave / p.wq;
   tc.slot = wqi * kLaneGroups + (lane >> 3);
@@ -505,10 +510,15 @@ __device__ __forceinline__ TileCoord tile_coord(const RowsParams& p) {
   return tc;
 }
 
-__device__ __forceinline__ void load_descriptors(const RowsParams& p, int64_t* desc) {
-  const int qt = static_cast<int>((blockIdx.x / p.nst) % p.nqt);
-  const int h = static_cast<int>((blockIdx.x / p.nst / p.nqt) % p.H);
+// Stages the tile's plane descriptors in LDS.  The leading barrier keeps a
+// workgroup that loops over tiles from overwriting descriptors another wave
+// is still reading.
+__device__ __forceinline__ void load_descriptors(const RowsParams& p, int64_t tile,
+                                                 int64_t* desc) {
+  const int qt = static_cast<int>((tile / p.nst) % p.nqt);
+  const int h = static_cast<int>((tile / p.nst / p.nqt) % p.H);
   const int n = p.wq * kWavePlanes;
+  __syncthreads();
   if (static_cast<int>(threadIdx.x) < n) {
     const int64_t c = static_cast<int64_t>(qt) * n + threadIdx.x;
     desc[threadIdx.x] = c < p.C ? p.planes[static_cast<int64_t>(h) * p.C + c] : -1;
@@ -555,10 +565,9 @@ __device__ __forceinline__ int64_t cursor_row(const RowsParams& p, int half, con
 // ---------------------------------------------------------------------------
 
 template <int BITS, bool ALIGNED>
-__global__ __launch_bounds__(kRowsThreads) void rows_unpack_kernel(RowsParams p) {
-  __shared__ int64_t desc[kTilePlanes];
-  load_descriptors(p, desc);
-  const TileCoord tc = tile_coord(p);
+__device__ __forceinline__ void unpack_tile(const RowsParams& p, int64_t tile,
+                                            const int64_t* desc) {
+  const TileCoord tc = tile_coord(p, tile);
   if (tc.q >= p.nq || tc.t0 >= p.row_tokens) return;
   const int64_t nv = p.T - tc.t0;  // tokens of this segment that hold symbols
   const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
@@ -606,10 +615,17 @@ __global__ __launch_bounds__(kRowsThreads) void rows_unpack_kernel(RowsParams p)
 }
 
 template <int BITS, bool ALIGNED>
-__global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
+__global__ __launch_bounds__(kRowsThreads) void rows_unpack_kernel(RowsParams p) {
   __shared__ int64_t desc[kTilePlanes];
-  load_descriptors(p, desc);
-  const TileCoord tc = tile_coord(p);
+  for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
+    load_descriptors(p, tile, desc);
+    unpack_tile<BITS, ALIGNED>(p, tile, desc);
+  }
+}
+
+template <int BITS, bool ALIGNED>
+__device__ __forceinline__ void pack_tile(const RowsParams& p, int64_t tile, const int64_t* desc) {
+  const TileCoord tc = tile_coord(p, tile);
   if (tc.q >= p.nq || tc.t0 >= p.T) return;
   const int nv = static_cast<int>(p.T - tc.t0 < 16 ? p.T - tc.t0 : 16);
 
@@ -647,6 +663,15 @@ __global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
     uint32_t u[NU > 4 ? NU : 4];
     compress16<BITS>(v[k], u);
     store_stream<ALIGNED>(p.stream + (P >> 3), u, nbytes);
+  }
+}
+
+template <int BITS, bool ALIGNED>
+__global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
+  __shared__ int64_t desc[kTilePlanes];
+  for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
+    load_descriptors(p, tile, desc);
+    pack_tile<BITS, ALIGNED>(p, tile, desc);
   }
 }
 
@@ -850,11 +875,14 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
   p.nst = static_cast<int32_t>((segs + segs_per_wg - 1) / segs_per_wg);
 }
 
-int launch_rows(bool pack, const RowsParams& p, int64_t nhalf, int bits, bool aligned,
+int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, bool aligned,
                 hipStream_t stream) {
-  const int64_t blocks = nhalf * p.H * static_cast<int64_t>(p.nqt) * p.nst;
-  if (blocks <= 0) return ORIGAMI_OK;
-  if (blocks > INT32_MAX) return fail(ORIGAMI_ERR_INVALID, "layer too large for one launch");
+  RowsParams p = params;
+  p.ntiles = nhalf * p.H * static_cast<int64_t>(p.nqt) * p.nst;
+  if (p.ntiles <= 0) return ORIGAMI_OK;
+  int64_t blocks = p.ntiles;
+  if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
+  if (blocks > INT32_MAX) blocks = INT32_MAX;
   const dim3 grid(static_cast<unsigned>(blocks)), block(kRowsThreads);
 #define ORIGAMI_ROWS_CASE(B)                                                           \
   case B:                                                                              \
@@ -914,6 +942,12 @@ extern "C" {
 const char* origami_last_error(void) { return g_last_error.c_str(); }
 
 int origami_abi_version(void) { return 1; }
+
+int64_t origami_set_rows_grid_limit(int64_t max_workgroups) {
+  const int64_t previous = g_rows_grid_limit;
+  g_rows_grid_limit = max_workgroups > 0 ? max_workgroups : 0;
+  return previous;
+}
 
 int origami_validate_chunks(const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
                             const int64_t* chunk_specs, int64_t num_chunks,

@@ -27,6 +27,7 @@ from typing import Callable
 
 import torch
 
+from origami_amd import _native
 from origami_amd.layout import CanonicalLayout
 from origami_amd.lossless import native_gpu
 
@@ -45,7 +46,7 @@ class LayerRestorePipeline:
     """Copy/compute-overlapped restore of one layer at a time into a cache."""
 
     def __init__(self, device: torch.device | str, slot_bytes: int, num_slots: int = 3,
-                 host_staging: bool = True):
+                 host_staging: bool = True, grid_limit: int = 0):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError("LayerRestorePipeline needs a ROCm device")
@@ -62,6 +63,10 @@ class LayerRestorePipeline:
             self._slots.append(_Slot(dev, host, torch.cuda.Event(), torch.cuda.Event()))
         self._next = 0
         self._lock = threading.Lock()
+        # Workgroup cap for the restore kernels: a restore hidden behind the
+        # next layer's copy needs no more than a share of the GPU, and a
+        # thinner launch leaves HBM bandwidth to the concurrent DMA.
+        self.grid_limit = int(grid_limit)
 
     # -- internals -----------------------------------------------------------
 
@@ -80,7 +85,11 @@ class LayerRestorePipeline:
         done = torch.cuda.Event()
         with torch.cuda.stream(self.compute_stream):
             self.compute_stream.wait_event(slot.copy_done)
-            compute(flat)
+            previous = _native.set_rows_grid_limit(self.grid_limit)
+            try:
+                compute(flat)
+            finally:
+                _native.set_rows_grid_limit(previous)
             slot.compute_done.record(self.compute_stream)
             slot.compute_recorded = True
             done.record(self.compute_stream)
