@@ -29,14 +29,21 @@ HBM_PEAK_GBPS = 8000.0
 METRIC = "KV restore GB/s (unpack+scatter) and % of HBM peak; per-layer restore µs"
 CAL_BYTES = 256 << 20
 
+# name -> (layers, tokens); both: 8 KV heads, head_dim 128, bf16, block_size 16
+WORKLOADS = {
+    "llama3-8b-32k": (32, 32768),      # Llama-3-8B geometry, one 32768-token request
+    "llama3-70b-128k": (80, 131072),   # Llama-3-70B geometry, one 131072-token request
+}
+
 
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--tokens", type=int, default=32768)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="llama3-8b-32k")
+    ap.add_argument("--layers", type=int, default=None)
+    ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--heads", type=int, default=8)
     ap.add_argument("--head-dim", type=int, default=128)
     ap.add_argument("--block-size", type=int, default=16)
@@ -52,6 +59,9 @@ def parse_args():
 
 def main() -> int:
     args = parse_args()
+    wl_layers, wl_tokens = WORKLOADS[args.workload]
+    args.layers = args.layers or wl_layers
+    args.tokens = args.tokens or wl_tokens
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the restore "
               "path needs no cross-GPU exchange and this build measures one GPU's share.",
@@ -199,7 +209,7 @@ def main() -> int:
         "dtype": "u8",
         "data": "synthetic",
         "config": {
-            "workload": (f"Llama-3-8B KV geometry layer-wise restore: {L} layers x {T} tokens, "
+            "workload": (f"{args.workload} KV geometry layer-wise restore: {L} layers x {T} tokens, "
                          f"{H} KV heads, head_dim {D}, bf16, block_size {bs}, permuted block "
                          f"table, 1 MiB chunks, bits {bits}; streams resident in HBM"),
             "layers": L, "tokens": T, "kv_heads": H, "head_dim": D, "block_size": bs,
