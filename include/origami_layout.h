@@ -2,9 +2,10 @@
  * origami_layout.h -- C ABI of the MI355X (gfx950) Origami KV codec-layout
  * library, liborigami_layout.so.
  *
- * The library replaces the layout/bitpack part of Origami's CUDA extension
- * (csrc/origami/bitpack_layout_cuda.cpp + bitpack_layout_cuda.cu, loaded as
- * `origami_bitpack_cuda_v6` by lossless/native_gpu.py:35-49).  Every entry
+ * The library replaces the layout/bitpack and fused-dequantize parts of
+ * Origami's CUDA extension (csrc/origami/bitpack_layout_cuda.cpp +
+ * bitpack_layout_cuda.cu, loaded as `origami_bitpack_cuda_v6` by
+ * lossless/native_gpu.py:35-49).  Every entry
  * point takes plain pointers and sizes: device buffers are raw device
  * addresses, metadata arrays are host memory, and the stream is a hipStream_t.
  * No torch types cross this boundary.
@@ -54,6 +55,11 @@ typedef struct ihipStream_t* origami_stream_t; /* == hipStream_t */
 
 #define ORIGAMI_CACHE_KV_FIRST 0
 #define ORIGAMI_CACHE_BLOCKS_FIRST 1
+
+/* element types of dequantize inputs and outputs */
+#define ORIGAMI_DTYPE_FLOAT16 1
+#define ORIGAMI_DTYPE_BFLOAT16 2
+#define ORIGAMI_DTYPE_FLOAT32 3
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* origami_last_error(void);
@@ -199,6 +205,56 @@ int origami_gather_kv_blocks(const void* kv_cache, int64_t cache_layout,
                              int64_t num_heads, int64_t head_bytes,
                              const int64_t* block_ids, int64_t block_count,
                              uint8_t* value, origami_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused dequantize paths (CacheGen).  Element types use the
+ * ORIGAMI_DTYPE_* codes; arithmetic is IEEE binary32 and results are
+ * rounded to nearest even into float16 / bfloat16.
+ * ------------------------------------------------------------------------- */
+
+/*
+ * CacheGen unpack + dequantize + paged scatter.  Replaces
+ * cachegen_unpack_dequantize_to_kv_cache_cuda (bitpack_layout_cuda.cpp:
+ * 475-581) and its kernel (bitpack_layout_cuda.cu:349-575).  The K and V
+ * streams are bytestream[key_offset, +key_bytes) and
+ * bytestream[value_offset, +value_bytes): symbol token * (heads * head_dim) +
+ * channel at key_bits / value_bits bits, LSB-first.  Destination element
+ * (block_ids[t / block_size], half, t % block_size, head, dim) becomes
+ * ((s - c) / c) * max[t] with c = bins / 2 - 1, for t < tokens; other tokens
+ * and ids outside [0, num_blocks) are left untouched.  max_key / max_value
+ * are device arrays of max_dtype (FLOAT16 or FLOAT32) with at least `tokens`
+ * values; kv_cache is FLOAT16 or BFLOAT16.  Stream bytes past key_bytes /
+ * value_bytes read as 0 at every width (the reference reads past the range
+ * unchecked at 8 bits).
+ */
+int origami_cachegen_unpack_dequantize_to_kv_cache(
+    const uint8_t* bytestream, int64_t bytestream_bytes, int64_t key_offset,
+    int64_t key_bytes, int64_t value_offset, int64_t value_bytes,
+    int64_t key_bits, int64_t value_bits, int64_t key_bins, int64_t value_bins,
+    const void* max_key, const void* max_value, int64_t max_key_count,
+    int64_t max_value_count, int64_t max_dtype, void* kv_cache,
+    int64_t cache_dtype, int64_t cache_layout, int64_t num_blocks,
+    int64_t block_size, const int64_t* block_ids, int64_t block_count,
+    int64_t tokens, int64_t heads, int64_t head_dim, origami_stream_t stream);
+
+/*
+ * CacheGen unpack + dequantize of several layers into a dense float16 tensor
+ * [layers, 2, heads, tokens, head_dim].  Replaces
+ * cachegen_unpack_dequantize_cuda (bitpack_layout_cuda.cpp:402-473) and its
+ * kernel (bitpack_layout_cuda.cu:141-186).  Host arrays: offsets[2 * layers +
+ * 1] (segment j < layers is layer j's keys, segment layers + j its values),
+ * bits_per_layer[2 * layers], key_bins[layers], value_bins[layers].  max_key
+ * and max_value are device arrays [layers, tokens] of max_dtype.  Offsets
+ * must be non-decreasing and within bytestream_bytes (a bound the reference
+ * lacks).
+ */
+int origami_cachegen_unpack_dequantize(
+    const uint8_t* bytestream, int64_t bytestream_bytes, const int64_t* offsets,
+    const int64_t* bits_per_layer, const int64_t* key_bins,
+    const int64_t* value_bins, int64_t layers, const void* max_key,
+    const void* max_value, int64_t max_key_count, int64_t max_value_count,
+    int64_t max_dtype, int64_t tokens, int64_t heads, int64_t head_dim,
+    void* output, int64_t output_bytes, origami_stream_t stream);
 
 #ifdef __cplusplus
 }

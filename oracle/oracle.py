@@ -1,4 +1,5 @@
-"""numpy/ctypes front end of the CPU oracle (oracle/layout_oracle.c).
+"""numpy/ctypes front end of the CPU oracle (oracle/layout_oracle.c and
+oracle/dequant_oracle.c).
 
 TEST INFRASTRUCTURE ONLY.  Imported by tests/, by __graft_entry__.smoke() as
 the checker, and by bench.py's cpu_baseline leg as the timed CPU baseline.
@@ -56,6 +57,22 @@ def lib() -> ctypes.CDLL:
             _u8p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
             ctypes.c_int, _i64p, ctypes.c_int64, _u8p]
         L.oracle_set_threads.argtypes = [ctypes.c_int]
+        L.oracle_dequant_last_error.restype = ctypes.c_char_p
+        L.oracle_half_to_float.restype = ctypes.c_float
+        L.oracle_half_to_float.argtypes = [ctypes.c_uint16]
+        L.oracle_float_to_half.restype = ctypes.c_uint16
+        L.oracle_float_to_half.argtypes = [ctypes.c_float]
+        L.oracle_float_to_bf16.restype = ctypes.c_uint16
+        L.oracle_float_to_bf16.argtypes = [ctypes.c_float]
+        _v, _i, _c = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.oracle_cachegen_to_kv_cache.argtypes = [
+            _u8p, _i, _i, _i, _i, _i, _c, _c, _i, _i, _v, _v, _c, _v, _c, _c, _i, _i, _i64p,
+            _i, _i, _i, _i]
+        L.oracle_cachegen_unpack_dequantize.argtypes = [
+            _u8p, _i, _i64p, _i64p, _i64p, _i64p, _i, _v, _v, _c, _i, _i, _i, _v]
+        L.oracle_kivi_to_kv_cache.argtypes = [
+            _u8p, _i, _i, _i, _i, _i, _c, _c, _i, _i, _v, _v, _v, _v, _v, _v, _c, _v, _c, _c,
+            _i, _i, _i64p, _i, _i, _i, _i]
         _lib = L
     return _lib
 
@@ -182,3 +199,97 @@ if os.environ.get("ORIGAMI_ORACLE_AUTOBUILD", "1") == "1" and not LIB_PATH.exist
         build()
     except Exception:  # built on demand by lib() again, which raises if it cannot
         pass
+
+
+# ---------------------------------------------------------------------------
+# Fused dequantize paths (dequant_oracle.c)
+# ---------------------------------------------------------------------------
+
+def _dq_check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(lib().oracle_dequant_last_error().decode())
+
+
+def half_to_float(bits: int) -> float:
+    return float(lib().oracle_half_to_float(int(bits)))
+
+
+def float_to_half(x: float) -> int:
+    return int(lib().oracle_float_to_half(float(x)))
+
+
+def float_to_bf16(x: float) -> int:
+    return int(lib().oracle_float_to_bf16(float(x)))
+
+
+def _meta(a: np.ndarray) -> tuple[np.ndarray, int]:
+    """float16 arrays travel as their bits; float32 as is."""
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.float16:
+        return a.view(np.uint16), 1
+    if a.dtype == np.float32:
+        return a, 0
+    raise TypeError("metadata must be float16 or float32")
+
+
+def _vp(a: np.ndarray) -> ctypes.c_void_p:
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def cachegen_to_kv_cache(bytestream, key_offset, key_bytes, value_offset, value_bytes,
+                         key_bits, value_bits, key_bins, value_bins, max_key, max_value,
+                         cache: np.ndarray, out_is_bf16: bool, blocks_first: bool, block_ids,
+                         tokens: int, heads: int, head_dim: int) -> None:
+    """In place on `cache` (uint16 bits of float16 / bfloat16, rank 5)."""
+    stream = np.ascontiguousarray(bytestream, dtype=np.uint8).reshape(-1)
+    mk, half = _meta(max_key)
+    mv, half_v = _meta(max_value)
+    assert half == half_v
+    ids = _i64(block_ids)
+    assert cache.dtype == np.uint16 and cache.flags.c_contiguous and cache.ndim == 5
+    nb = cache.shape[0] if blocks_first else cache.shape[1]
+    _dq_check(lib().oracle_cachegen_to_kv_cache(
+        _p8(stream), stream.size, int(key_offset), int(key_bytes), int(value_offset),
+        int(value_bytes), int(key_bits), int(value_bits), int(key_bins), int(value_bins),
+        _vp(mk), _vp(mv), half, _vp(cache), int(bool(out_is_bf16)), int(bool(blocks_first)),
+        int(nb), int(cache.shape[2]), _p64(ids), ids.size, int(tokens), int(heads),
+        int(head_dim)))
+
+
+def cachegen_unpack_dequantize(bytestream, offsets, bits_per_layer, key_bins, value_bins,
+                               max_key, max_value, tokens: int, heads: int,
+                               head_dim: int) -> np.ndarray:
+    """Returns float16 [layers, 2, heads, tokens, head_dim]."""
+    stream = np.ascontiguousarray(bytestream, dtype=np.uint8).reshape(-1)
+    offs, bits = _i64(offsets), _i64(bits_per_layer)
+    kb, vb = _i64(key_bins), _i64(value_bins)
+    layers = bits.size // 2
+    mk, half = _meta(max_key)
+    mv, _ = _meta(max_value)
+    out = np.zeros((layers, 2, heads, tokens, head_dim), dtype=np.uint16)
+    _dq_check(lib().oracle_cachegen_unpack_dequantize(
+        _p8(stream), stream.size, _p64(offs), _p64(bits), _p64(kb), _p64(vb), layers,
+        _vp(mk), _vp(mv), half, int(tokens), int(heads), int(head_dim), _vp(out)))
+    return out.view(np.float16)
+
+
+def kivi_to_kv_cache(bytestream, key_offset, key_bytes, value_offset, value_bytes, bits,
+                     nibble3: bool, group_size, sink_tokens, key_scale, key_zero, value_scale,
+                     value_zero, key_sink, value_sink, cache: np.ndarray, out_is_bf16: bool,
+                     blocks_first: bool, block_ids, tokens: int, heads: int,
+                     head_dim: int) -> None:
+    """In place on `cache` (uint16 bits of float16 / bfloat16, rank 5)."""
+    stream = np.ascontiguousarray(bytestream, dtype=np.uint8).reshape(-1)
+    metas = [_meta(a) for a in (key_scale, key_zero, value_scale, value_zero, key_sink,
+                                value_sink)]
+    half = metas[0][1]
+    assert all(m[1] == half for m in metas)
+    ids = _i64(block_ids)
+    assert cache.dtype == np.uint16 and cache.flags.c_contiguous and cache.ndim == 5
+    nb = cache.shape[0] if blocks_first else cache.shape[1]
+    _dq_check(lib().oracle_kivi_to_kv_cache(
+        _p8(stream), stream.size, int(key_offset), int(key_bytes), int(value_offset),
+        int(value_bytes), int(bits), int(bool(nibble3)), int(group_size), int(sink_tokens),
+        *[_vp(m[0]) for m in metas], half, _vp(cache), int(bool(out_is_bf16)),
+        int(bool(blocks_first)), int(nb), int(cache.shape[2]), _p64(ids), ids.size,
+        int(tokens), int(heads), int(head_dim)))

@@ -12,7 +12,7 @@ from pathlib import Path
 import numpy as np
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liborigami_layout.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 ORIGAMI_OK = 0
 ORIGAMI_ERR_INVALID = 1
@@ -21,6 +21,10 @@ ORIGAMI_ERR_HIP = 3
 
 CACHE_KV_FIRST = 0
 CACHE_BLOCKS_FIRST = 1
+
+DTYPE_FLOAT16 = 1
+DTYPE_BFLOAT16 = 2
+DTYPE_FLOAT32 = 3
 
 _i64 = ctypes.c_int64
 _p = ctypes.c_void_p
@@ -41,6 +45,11 @@ _SIGNATURES: dict[str, list] = {
         _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _i64, _p],
     "origami_scatter_kv_blocks": [_p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "origami_gather_kv_blocks": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p, _p],
+    "origami_cachegen_unpack_dequantize_to_kv_cache": [
+        _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _i64, _i64,
+        _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p],
+    "origami_cachegen_unpack_dequantize": [
+        _p, _i64, _p, _p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
 }
 
 EXPORTED_SYMBOLS = ("origami_last_error", *_SIGNATURES)

@@ -13,7 +13,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 REPO = PKG.parent
-SRC = PKG / "csrc" / "origami_layout.hip"
+SOURCES = [PKG / "csrc" / "origami_layout.hip", PKG / "csrc" / "origami_dequant.hip"]
 INCLUDE = REPO / "include"
 LIB_DIR = PKG / "_lib"
 LIB_PATH = LIB_DIR / "liborigami_layout.so"
@@ -26,6 +26,9 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-shared",
     "-Wall",
+    # no implicit contraction: float results round exactly where the source
+    # rounds (fused multiply-adds are written out as fmaf)
+    "-ffp-contract=off",
     # packed FP32 VALU forms are disabled for all device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
@@ -41,7 +44,7 @@ def hipcc() -> str:
 def build(verbose: bool = False) -> Path:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", str(SRC), "-o", str(tmp)]
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", *map(str, SOURCES), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

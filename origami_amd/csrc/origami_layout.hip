@@ -33,20 +33,16 @@
 #include <unordered_map>
 #include <vector>
 
+#include "origami_internal.h"
 #include "origami_layout.h"
 
-namespace {
+// ---------------------------------------------------------------------------
+// Errors and shared host helpers (declared in origami_internal.h)
+// ---------------------------------------------------------------------------
 
-// ---------------------------------------------------------------------------
-// Errors
-// ---------------------------------------------------------------------------
+namespace origami_internal {
 
 thread_local std::string g_last_error;
-
-// Upper bound on the workgroups of one rows-kernel launch on this thread
-// (0: one workgroup per tile).  A restore that runs hidden behind other work
-// can be spread thinner over the GPU with it.
-thread_local int64_t g_rows_grid_limit = 0;
 
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
@@ -61,10 +57,31 @@ int check_launch(const char* what) {
   return ORIGAMI_OK;
 }
 
-#define ORIGAMI_REQUIRE(cond, msg)              \
-  do {                                          \
-    if (!(cond)) return fail(ORIGAMI_ERR_INVALID, msg); \
-  } while (0)
+int cache_geometry(int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+                   int64_t* blk_stride, int64_t* half_stride) {
+  if (cache_layout == ORIGAMI_CACHE_KV_FIRST) {
+    *blk_stride = block_size;               // [2, NB, bs, H, D]
+    *half_stride = num_blocks * block_size;
+  } else if (cache_layout == ORIGAMI_CACHE_BLOCKS_FIRST) {
+    *blk_stride = 2 * block_size;           // [NB, 2, bs, H, D]
+    *half_stride = block_size;
+  } else {
+    return fail(ORIGAMI_ERR_INVALID,
+                "kv_cache must be [num_blocks,2,block,heads,dim] or [2,num_blocks,block,heads,dim]");
+  }
+  return ORIGAMI_OK;
+}
+
+}  // namespace origami_internal
+
+using namespace origami_internal;
+
+namespace {
+
+// Upper bound on the workgroups of one rows-kernel launch on this thread
+// (0: one workgroup per tile).  A restore that runs hidden behind other work
+// can be spread thinner over the GPU with it.
+thread_local int64_t g_rows_grid_limit = 0;
 
 // ---------------------------------------------------------------------------
 // Host-side layout helpers
@@ -825,15 +842,6 @@ __global__ __launch_bounds__(kThreads) void block_copy_kernel(BlockCopyParams p)
 // Launch helpers
 // ---------------------------------------------------------------------------
 
-bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
-
-unsigned grid_for(int64_t work, int64_t per_block, int64_t cap) {
-  int64_t g = (work + per_block - 1) / per_block;
-  if (g < 1) g = 1;
-  if (g > cap) g = cap;
-  return static_cast<unsigned>(g);
-}
-
 int launch_fill_zero(uint8_t* p, int64_t n, hipStream_t stream) {
   if (n <= 0) return ORIGAMI_OK;
   if (aligned16(p)) {
@@ -914,21 +922,6 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, bo
   return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
 }
 
-int cache_geometry(int64_t cache_layout, int64_t num_blocks, int64_t block_size,
-                   int64_t* blk_stride, int64_t* half_stride) {
-  if (cache_layout == ORIGAMI_CACHE_KV_FIRST) {
-    *blk_stride = block_size;               // [2, NB, bs, H, D]
-    *half_stride = num_blocks * block_size;
-  } else if (cache_layout == ORIGAMI_CACHE_BLOCKS_FIRST) {
-    *blk_stride = 2 * block_size;           // [NB, 2, bs, H, D]
-    *half_stride = block_size;
-  } else {
-    return fail(ORIGAMI_ERR_INVALID,
-                "kv_cache must be [num_blocks,2,block,heads,dim] or [2,num_blocks,block,heads,dim]");
-  }
-  return ORIGAMI_OK;
-}
-
 const int64_t kKvAxes[4] = {0, 1, 2, -1};
 
 }  // namespace
@@ -941,7 +934,7 @@ extern "C" {
 
 const char* origami_last_error(void) { return g_last_error.c_str(); }
 
-int origami_abi_version(void) { return 1; }
+int origami_abi_version(void) { return 2; }
 
 int64_t origami_set_rows_grid_limit(int64_t max_workgroups) {
   const int64_t previous = g_rows_grid_limit;

@@ -1,9 +1,10 @@
 """GPU layout path: Python front end of liborigami_layout.so.
 
 Mirrors lossless/native_gpu.py of the reference (load_bitpack_cuda_extension,
-available, unpack_canonical_storage_chunks; native_gpu.py:35-146) and adds the
-pieces the reference lacks: the pack, the fused unpack+scatter into the paged
-KV cache and the fused gather+pack from it.
+available, unpack_canonical_storage_chunks, cachegen_unpack_dequantize*;
+native_gpu.py:35-215) and adds the pieces the reference lacks: the pack, the
+fused unpack+scatter into the paged KV cache and the fused gather+pack from
+it.
 
 All work is enqueued on the calling thread's current stream of the tensors'
 device, like the reference (bitpack_layout_cuda.cpp:370).  Chunk metadata stays
@@ -328,6 +329,127 @@ def gather_kv_blocks(kv_cache: torch.Tensor, block_ids: torch.Tensor,
 
 
 # ---------------------------------------------------------------------------
+# Fused dequantize paths (CacheGen)
+# ---------------------------------------------------------------------------
+
+_DTYPE_CODES = {
+    torch.float16: _native.DTYPE_FLOAT16,
+    torch.bfloat16: _native.DTYPE_BFLOAT16,
+    torch.float32: _native.DTYPE_FLOAT32,
+}
+
+
+def dequant_cache_geometry(kv_cache: torch.Tensor, heads: int, head_dim: int
+                           ) -> tuple[int, int, int]:
+    """(layout code, num_blocks, block_size) for the fused dequantize paths.
+    These follow bitpack_layout_cuda.cpp:526-552, which recognises
+    [NB, 2, bs, H, D] first and [2, NB, bs, H, D] second (the opposite
+    order from cache_geometry)."""
+    if kv_cache.dim() != 5:
+        raise RuntimeError("kv_cache must have rank 5")
+    if int(kv_cache.shape[1]) == 2:
+        code, nb = CACHE_BLOCKS_FIRST, int(kv_cache.shape[0])
+    elif int(kv_cache.shape[0]) == 2:
+        code, nb = CACHE_KV_FIRST, int(kv_cache.shape[1])
+    else:
+        raise RuntimeError("kv_cache must be [num_blocks,2,block,heads,dim] or "
+                           "[2,num_blocks,block,heads,dim]")
+    if int(kv_cache.shape[3]) != int(heads) or int(kv_cache.shape[4]) != int(head_dim):
+        raise RuntimeError("kv_cache head shape mismatch")
+    return code, nb, int(kv_cache.shape[2])
+
+
+def _max_tensors(max_key: torch.Tensor, max_value: torch.Tensor) -> int:
+    _require_cuda(max_key, "max_key")
+    _require_cuda(max_value, "max_value")
+    if max_key.dtype != max_value.dtype:
+        raise RuntimeError("max_key and max_value must have the same dtype")
+    if max_key.dtype not in (torch.float16, torch.float32):
+        raise RuntimeError("max tensors must be float16 or float32")
+    return _DTYPE_CODES[max_key.dtype]
+
+
+def cachegen_unpack_dequantize_to_kv_cache(
+    bytestream: torch.Tensor, *, key_offset: int, key_bytes: int, value_offset: int,
+    value_bytes: int, key_bits: int, value_bits: int, key_bins: int, value_bins: int,
+    max_key: torch.Tensor, max_value: torch.Tensor, kv_cache: torch.Tensor,
+    block_ids: torch.Tensor, tokens: int, heads: int, head_dim: int,
+) -> None:
+    """CacheGen fused restore into the paged cache (native_gpu.py:178-215,
+    bitpack_layout_cuda.cpp:475-581): the K and V streams are unpacked,
+    dequantized ((s - c) / c * max[token]) and written to the listed blocks
+    in one kernel per half.  Tokens >= `tokens` are left untouched."""
+    flat = bytestream.reshape(-1)
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    _require_cuda(flat, "bytestream")
+    if flat.dtype != torch.uint8:
+        raise RuntimeError("bytestream must be uint8")
+    _require_cuda(kv_cache, "kv_cache")
+    if kv_cache.dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError("kv_cache must be float16 or bfloat16")
+    max_key, max_value = max_key.contiguous(), max_value.contiguous()
+    max_code = _max_tensors(max_key, max_value)
+    ids = block_ids.to(device=kv_cache.device, dtype=torch.int64).contiguous()
+    code, nb, bs = dequant_cache_geometry(kv_cache, heads, head_dim)
+    with torch.cuda.device(kv_cache.device):
+        _native.call(
+            "origami_cachegen_unpack_dequantize_to_kv_cache",
+            flat.data_ptr(), flat.numel(), int(key_offset), int(key_bytes), int(value_offset),
+            int(value_bytes), int(key_bits), int(value_bits), int(key_bins), int(value_bins),
+            max_key.data_ptr(), max_value.data_ptr(), max_key.numel(), max_value.numel(),
+            max_code, kv_cache.data_ptr(), _DTYPE_CODES[kv_cache.dtype], code, nb, bs,
+            ids.data_ptr(), ids.numel(), int(tokens), int(heads), int(head_dim),
+            _stream_handle(kv_cache.device))
+
+
+def _host_i64(values) -> np.ndarray:
+    if isinstance(values, torch.Tensor):
+        values = values.detach().to("cpu", torch.int64).reshape(-1).numpy()
+    return _native.i64_array(values)
+
+
+def cachegen_unpack_dequantize(
+    bytestream: torch.Tensor, offsets, bits_per_layer, key_bins, value_bins,
+    max_key: torch.Tensor, max_value: torch.Tensor, *, tokens: int, heads: int, head_dim: int,
+) -> torch.Tensor:
+    """CacheGen unpack + dequantize of `layers` layers into a float16 tensor
+    [layers, 2, heads, tokens, head_dim] (native_gpu.py:149-175,
+    bitpack_layout_cuda.cpp:402-473).  Stream segment j of `offsets` is
+    layer j's keys for j < layers and layer j - layers' values after that."""
+    flat = bytestream.reshape(-1)
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    _require_cuda(flat, "bytestream")
+    if flat.dtype != torch.uint8:
+        raise RuntimeError("bytestream must be uint8")
+    offs, bits = _host_i64(offsets), _host_i64(bits_per_layer)
+    kb, vb = _host_i64(key_bins), _host_i64(value_bins)
+    if bits.size % 2:
+        raise RuntimeError("bits_per_layer length must be even")
+    layers = bits.size // 2
+    if kb.size != layers:
+        raise RuntimeError("key_bins length must match layers")
+    if vb.size != layers:
+        raise RuntimeError("value_bins length must match layers")
+    if offs.size != bits.size + 1:
+        raise RuntimeError("offsets length must be bits_per_layer length + 1")
+    max_key, max_value = max_key.contiguous(), max_value.contiguous()
+    max_code = _max_tensors(max_key, max_value)
+    out = torch.empty((layers, 2, int(heads), int(tokens), int(head_dim)), dtype=torch.float16,
+                      device=flat.device)
+    with torch.cuda.device(flat.device):
+        _native.call(
+            "origami_cachegen_unpack_dequantize",
+            flat.data_ptr(), flat.numel(), _native.host_ptr(offs), _native.host_ptr(bits),
+            _native.host_ptr(kb), _native.host_ptr(vb), layers, max_key.data_ptr(),
+            max_value.data_ptr(), max_key.numel(), max_value.numel(), max_code, int(tokens),
+            int(heads), int(head_dim), out.data_ptr(), out.numel() * 2,
+            _stream_handle(flat.device))
+    return out
+
+
+# ---------------------------------------------------------------------------
 # Reference extension surface (origami_bitpack_cuda_v6, cpp:894-903)
 # ---------------------------------------------------------------------------
 
@@ -369,16 +491,39 @@ class _Extension:
         return unpack_layout(flat, layout)
 
     @staticmethod
-    def cachegen_unpack_dequantize_to_kv_cache_cuda(*args: Any, **kwargs: Any) -> None:
-        raise NotImplementedError("CacheGen dequantize-to-cache is not part of this build yet")
+    def cachegen_unpack_dequantize_to_kv_cache_cuda(
+        bytestream: torch.Tensor, key_offset: int, key_bytes: int, value_offset: int,
+        value_bytes: int, key_bits: int, value_bits: int, key_bins: int, value_bins: int,
+        max_key: torch.Tensor, max_value: torch.Tensor, kv_cache: torch.Tensor,
+        block_ids: torch.Tensor, tokens: int, heads: int, head_dim: int,
+    ) -> None:
+        """Signature of bitpack_layout_cuda.cpp:475-491."""
+        for t, name in ((bytestream, "bytestream"), (block_ids, "block_ids")):
+            _require_cuda(t, name)
+        if block_ids.dtype != torch.int64:
+            raise RuntimeError("block_ids must be int64")
+        cachegen_unpack_dequantize_to_kv_cache(
+            bytestream, key_offset=key_offset, key_bytes=key_bytes, value_offset=value_offset,
+            value_bytes=value_bytes, key_bits=key_bits, value_bits=value_bits,
+            key_bins=key_bins, value_bins=value_bins, max_key=max_key, max_value=max_value,
+            kv_cache=kv_cache, block_ids=block_ids, tokens=tokens, heads=heads,
+            head_dim=head_dim)
 
     @staticmethod
     def kivi_dequantize_to_kv_cache_cuda(*args: Any, **kwargs: Any) -> None:
         raise NotImplementedError("KIVI dequantize-to-cache is not part of this build yet")
 
     @staticmethod
-    def cachegen_unpack_dequantize_cuda(*args: Any, **kwargs: Any) -> torch.Tensor:
-        raise NotImplementedError("CacheGen unpack-dequantize is not part of this build yet")
+    def cachegen_unpack_dequantize_cuda(
+        bytestream: torch.Tensor, offsets: torch.Tensor, bits_per_layer: torch.Tensor,
+        key_bins: torch.Tensor, value_bins: torch.Tensor, max_key: torch.Tensor,
+        max_value: torch.Tensor, tokens: int, heads: int, head_dim: int,
+    ) -> torch.Tensor:
+        """Signature of bitpack_layout_cuda.cpp:402-412."""
+        _require_cuda(bytestream, "bytestream")
+        return cachegen_unpack_dequantize(
+            bytestream, offsets, bits_per_layer, key_bins, value_bins, max_key, max_value,
+            tokens=tokens, heads=heads, head_dim=head_dim)
 
     @staticmethod
     def fused_prefix_attention_cuda(*args: Any, **kwargs: Any) -> None:
@@ -401,4 +546,6 @@ __all__ = [
     "pack_canonical_storage_flat", "unpack_layout", "pack_layout", "cache_geometry",
     "block_ids_tensor", "unpack_to_kv_cache", "pack_from_kv_cache", "scatter_kv_blocks",
     "gather_kv_blocks", "kv_symbol_layout", "CACHE_KV_FIRST", "CACHE_BLOCKS_FIRST",
+    "cachegen_unpack_dequantize_to_kv_cache", "cachegen_unpack_dequantize",
+    "dequant_cache_geometry",
 ]
