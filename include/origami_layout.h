@@ -61,6 +61,12 @@ typedef struct ihipStream_t* origami_stream_t; /* == hipStream_t */
 #define ORIGAMI_DTYPE_BFLOAT16 2
 #define ORIGAMI_DTYPE_FLOAT32 3
 
+/* KIVI symbol packing: LSB-first at `bits` bits (what the reference kernel
+ * reads), or KIVI's own container, where 3-bit symbols sit one per nibble
+ * (kivi_adapter.py:39-43) and other widths are LSB-first. */
+#define ORIGAMI_KIVI_PACKED_LSB 0
+#define ORIGAMI_KIVI_NIBBLE3 1
+
 /* Message of the last failing call on this thread ("" if none). */
 const char* origami_last_error(void);
 
@@ -207,7 +213,7 @@ int origami_gather_kv_blocks(const void* kv_cache, int64_t cache_layout,
                              uint8_t* value, origami_stream_t stream);
 
 /* ---------------------------------------------------------------------------
- * Fused dequantize paths (CacheGen).  Element types use the
+ * Fused dequantize paths (CacheGen, KIVI).  Element types use the
  * ORIGAMI_DTYPE_* codes; arithmetic is IEEE binary32 and results are
  * rounded to nearest even into float16 / bfloat16.
  * ------------------------------------------------------------------------- */
@@ -255,6 +261,34 @@ int origami_cachegen_unpack_dequantize(
     const void* max_value, int64_t max_key_count, int64_t max_value_count,
     int64_t max_dtype, int64_t tokens, int64_t heads, int64_t head_dim,
     void* output, int64_t output_bytes, origami_stream_t stream);
+
+/*
+ * KIVI dequantize + paged scatter.  Replaces kivi_dequantize_to_kv_cache_cuda
+ * (bitpack_layout_cuda.cpp:583-714) and its kernel (bitpack_layout_cuda.cu:
+ * 578-853).  Tokens [0, sink_tokens) copy key_sink / value_sink ([sink, C]);
+ * body token bt = t - sink_tokens reads, for keys, symbol (d * heads + h) *
+ * body + bt and dequantizes fmaf(s, key_scale[bt / group][c],
+ * key_zero[bt / group][c]); for values, symbol (h * head_dim + d) * body + bt
+ * and fmaf(s, value_scale[bt][c / group], value_zero[bt][c / group]), with
+ * body = tokens - sink_tokens and C = heads * head_dim.  The reference's
+ * `s * scale + zero` is one fused multiply-add as nvcc compiles it.
+ * meta_counts (host, [6]) are the element counts of key_scale, key_zero,
+ * value_scale, value_zero, key_sink, value_sink; the metadata arrays are
+ * device arrays of meta_dtype (FLOAT16 or FLOAT32), aligned to their element
+ * size.  symbol_packing is ORIGAMI_KIVI_PACKED_LSB or ORIGAMI_KIVI_NIBBLE3.
+ * Destination handling is that of the CacheGen entry point: tokens >= tokens
+ * and invalid block ids are left untouched.
+ */
+int origami_kivi_dequantize_to_kv_cache(
+    const uint8_t* bytestream, int64_t bytestream_bytes, int64_t key_offset,
+    int64_t key_bytes, int64_t value_offset, int64_t value_bytes, int64_t bits,
+    int64_t symbol_packing, int64_t group_size, int64_t sink_tokens,
+    const void* key_scale, const void* key_zero, const void* value_scale,
+    const void* value_zero, const void* key_sink, const void* value_sink,
+    const int64_t* meta_counts, int64_t meta_dtype, void* kv_cache,
+    int64_t cache_dtype, int64_t cache_layout, int64_t num_blocks,
+    int64_t block_size, const int64_t* block_ids, int64_t block_count,
+    int64_t tokens, int64_t heads, int64_t head_dim, origami_stream_t stream);
 
 #ifdef __cplusplus
 }

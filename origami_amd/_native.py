@@ -26,6 +26,9 @@ DTYPE_FLOAT16 = 1
 DTYPE_BFLOAT16 = 2
 DTYPE_FLOAT32 = 3
 
+KIVI_PACKED_LSB = 0
+KIVI_NIBBLE3 = 1
+
 _i64 = ctypes.c_int64
 _p = ctypes.c_void_p
 
@@ -50,6 +53,9 @@ _SIGNATURES: dict[str, list] = {
         _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p],
     "origami_cachegen_unpack_dequantize": [
         _p, _i64, _p, _p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "origami_kivi_dequantize_to_kv_cache": [
+        _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p,
+        _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p],
 }
 
 EXPORTED_SYMBOLS = ("origami_last_error", *_SIGNATURES)

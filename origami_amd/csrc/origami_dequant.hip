@@ -1,6 +1,7 @@
 // origami_dequant.hip -- MI355X (gfx950) kernels and C ABI for Origami's fused
 // dequantize paths: CacheGen unpack + dequantize (into the paged KV cache, and
-// into a dense [layers, 2, heads, tokens, head_dim] tensor).
+// into a dense [layers, 2, heads, tokens, head_dim] tensor) and KIVI
+// dequantize into the paged KV cache.
 //
 // CacheGen streams (csrc/origami/bitpack_layout_cuda.cu:349-423) hold one
 // half's symbols token-major, symbol token * C + channel at b bits LSB-first,
@@ -104,6 +105,32 @@ __device__ __forceinline__ uint32_t out_bits(float v) {
   }
 }
 
+// Two binary32 values rounded to nearest even and packed (a low, b high);
+// one v_cvt_pk conversion for both.  The empty asm serves as in out_bits.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t out_bits2(float a, float b) {
+  asm("" : "+v"(a), "+v"(b));
+  const f32x2 v = {a, b};
+  if constexpr (BF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  }
+}
+
+// fmaf(a, b, c) as a three-address v_fma_f32: the addend (a zero point shared
+// by many elements) stays in its register instead of being copied into the
+// accumulator of a two-address v_fmac for every element.
+__device__ __forceinline__ float fma3(float a, float b, float c) {
+  float r;
+  asm("v_fma_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // (s - c) / c for s in [0, 2^bits), correctly rounded (the reference's
 // `((float)s - center) / center`, bitpack_layout_cuda.cu:401-403).
 __device__ __forceinline__ float cachegen_level(int s, float center) {
@@ -157,7 +184,7 @@ __global__ __launch_bounds__(kDqThreads) void cachegen_cache_kernel(CacheGenCach
       for (int k = 0; k < 4; ++k) {
         const uint32_t s0 = static_cast<uint32_t>(w >> ((2 * k) * BITS)) & mask;
         const uint32_t s1 = static_cast<uint32_t>(w >> ((2 * k + 1) * BITS)) & mask;
-        o[k] = out_bits<BF16>(lut[s0] * m) | (out_bits<BF16>(lut[s1] * m) << 16);
+        o[k] = out_bits2<BF16>(lut[s0] * m, lut[s1] * m);
       }
       const u32x4 x = {o[0], o[1], o[2], o[3]};
       __builtin_nontemporal_store(
@@ -284,6 +311,268 @@ __global__ __launch_bounds__(kDqThreads) void cachegen_dense_generic_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// KIVI -> paged KV cache
+// ---------------------------------------------------------------------------
+//
+// KIVI streams (bitpack_layout_cuda.cu:578-683, kivi_adapter.py:97-122) hold
+// the body tokens [sink, tokens) plane-major with the token axis fastest:
+// keys in plane order (head_dim, head), values in (head, head_dim).  Plane
+// p's run starts at bit p * body * b.  Keys are dequantized per channel with
+// groups along tokens (scale[bt / group][c]), values per token with groups
+// along channels (scale[bt][c / group]); value = fmaf(s, scale, zero).
+//
+// Row kernel (C and head_dim multiples of 8, group a multiple of 16, block
+// size >= 16): a lane owns 8 channels x LT body tokens (LT = 16, or 32 at odd
+// widths, so that its run of one plane is whole dwords).  It reads that run
+// of each of its 8 planes with dword loads (funnel-shifted when the plane
+// does not start on a dword), keeps it packed, and for every token extracts
+// the 8 symbols, dequantizes them and writes one 16-byte store.  Eight lanes
+// along channels cover a 128-byte line of a destination row; eight lanes
+// along tokens read 8 * LT consecutive tokens of a plane.  A workgroup (2
+// waves along channels) is 8 * LT tokens x 128 channels; the value metadata
+// of its tokens is staged in LDS.
+
+constexpr int kKiviWavesC = 2;
+constexpr int kKiviThreads = 64 * kKiviWavesC;
+constexpr int kKiviTileChannels = 64 * kKiviWavesC;
+constexpr int kKiviMaxGroups = kKiviTileChannels / 16;  // value groups per tile (group >= 16)
+
+// Body tokens per lane at `sbits` stored bits per symbol: the fewest that
+// make a lane's plane run whole dwords (LT * sbits a multiple of 32).  More
+// tokens per lane read longer runs but leave fewer waves to hide latency,
+// which measured slower.
+constexpr int kivi_lane_tokens(int sbits) { return sbits % 2 == 1 ? 32 : 16; }
+
+struct KiviHalf {
+  const uint8_t* sbase;  // 4-byte aligned base of the half's stream
+  int64_t sbytes;        // readable bytes from sbase
+  int64_t bit_bias;      // (stream start - sbase) * 8
+  const void* scale;
+  const void* zero;
+  const void* sink;
+};
+
+struct KiviParams {
+  KiviHalf half[2];      // 0: keys, 1: values
+  uint16_t* cache;
+  const int64_t* block_ids;
+  int64_t num_blocks, bs, blk_stride, half_stride;
+  int64_t sink, body;
+  int64_t C, H, D;
+  int64_t group, vgroups;
+  int32_t nct;           // workgroups along channels
+};
+
+// Row index of token t of `half`, or -1 when its block id is outside the cache.
+__device__ __forceinline__ int64_t kivi_row(const KiviParams& p, int half, int64_t blk,
+                                            int64_t off) {
+  const int64_t pid = p.block_ids[blk];
+  if (pid < 0 || pid >= p.num_blocks) return -1;
+  return pid * p.blk_stride + half * p.half_stride + off;
+}
+
+template <int SBITS, bool NIB3, bool BF16, bool META_HALF>
+__global__ __launch_bounds__(kKiviThreads) void kivi_cache_kernel(KiviParams p) {
+  constexpr int LT = kivi_lane_tokens(SBITS);
+  constexpr int NU = LT * SBITS / 32;  // packed dwords of a lane's plane run
+  constexpr int TILE_T = 8 * LT;
+  constexpr uint32_t mask = NIB3 ? 0x7u : (1u << SBITS) - 1u;
+  __shared__ float vmeta[2][kKiviMaxGroups][TILE_T];
+  const int half = blockIdx.y;
+  const KiviHalf& hs = p.half[half];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ct = static_cast<int>(blockIdx.x % p.nct);
+  const int64_t tile_bt0 = static_cast<int64_t>(blockIdx.x / p.nct) * TILE_T;
+  const int64_t tile_c0 = static_cast<int64_t>(ct) * kKiviTileChannels;
+  const int64_t c0 = tile_c0 + wave * 64 + (lane & 7) * 8;
+  const int64_t bt0 = tile_bt0 + (lane >> 3) * LT;
+
+  // Value metadata of the tile: [scale / zero][group][token], staged once
+  // (consecutive threads read consecutive groups of a token).
+  const int64_t g_first = tile_c0 / p.group;
+  if (half == 1) {
+    const int64_t c_last = min(tile_c0 + kKiviTileChannels, p.C) - 1;
+    const int ng = static_cast<int>(c_last / p.group - g_first + 1);
+    for (int i = threadIdx.x; i < ng * TILE_T; i += kKiviThreads) {
+      const int tt = i / ng, gi = i - tt * ng;
+      const int64_t bt = tile_bt0 + tt;
+      float sc = 0.f, ze = 0.f;
+      if (bt < p.body) {
+        const int64_t mi = bt * p.vgroups + g_first + gi;
+        sc = load_meta<META_HALF>(hs.scale, mi);
+        ze = load_meta<META_HALF>(hs.zero, mi);
+      }
+      vmeta[0][gi][tt] = sc;
+      vmeta[1][gi][tt] = ze;
+    }
+    __syncthreads();
+  }
+  if (c0 >= p.C || bt0 >= p.body) return;
+
+  // The lane's runs of its 8 planes, packed.  Key planes of consecutive
+  // channels are H planes apart, value planes adjacent.
+  const int64_t h = c0 / p.D, d0 = c0 - h * p.D;  // D % 8 == 0: one head
+  const int64_t plane0 = half == 0 ? d0 * p.H + h : c0;
+  const int64_t pstep = (half == 0 ? p.H : 1) * p.body * SBITS;
+  int64_t P = hs.bit_bias + (plane0 * p.body + bt0) * SBITS;
+  uint32_t u[8][NU];
+#pragma unroll
+  for (int i = 0; i < 8; ++i, P += pstep) {
+    const int64_t byte0 = (P >> 5) * 4;
+    const uint32_t sh = static_cast<uint32_t>(P & 31);
+    uint32_t w[NU + 1];
+    if (byte0 + 4 * (NU + 1) <= hs.sbytes) {
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(hs.sbase + byte0);
+#pragma unroll
+      for (int k = 0; k <= NU; ++k) w[k] = src[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k <= NU; ++k) w[k] = load_dword_guarded(hs.sbase, byte0 + 4 * k, hs.sbytes);
+    }
+#pragma unroll
+    for (int k = 0; k < NU; ++k) u[i][k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
+  }
+
+  const int nj = static_cast<int>(min<int64_t>(LT, p.body - bt0));
+  const int gi = static_cast<int>(c0 / p.group - g_first);
+  const int tt0 = static_cast<int>(bt0 - tile_bt0);
+
+  // 16-token chunks: each lies in one key group (group % 16 == 0) and in at
+  // most two blocks (block_size >= 16).
+#pragma unroll
+  for (int jb = 0; jb < LT / 16; ++jb) {
+    if (16 * jb >= nj) break;
+    float ks[8] = {}, kz[8] = {};
+    if (half == 0) {
+      const int64_t g = (bt0 + 16 * jb) / p.group;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        ks[i] = load_meta<META_HALF>(hs.scale, g * p.C + c0 + i);
+        kz[i] = load_meta<META_HALF>(hs.zero, g * p.C + c0 + i);
+      }
+    }
+    const int64_t t0 = p.sink + bt0 + 16 * jb;
+    const int64_t blk0 = t0 / p.bs;
+    const int64_t off0 = t0 - blk0 * p.bs;
+    const int jsplit = static_cast<int>(min<int64_t>(16, p.bs - off0));
+    const int64_t row_a = kivi_row(p, half, blk0, off0);
+    const int64_t row_b = jsplit < nj - 16 * jb ? kivi_row(p, half, blk0 + 1, 0) : -1;
+    uint16_t* const dst_a = p.cache + row_a * p.C + c0;
+    uint16_t* const dst_b = p.cache + row_b * p.C + c0;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      const int j = 16 * jb + jj;
+      const bool second = jj >= jsplit;
+      if (j < nj && (second ? row_b : row_a) >= 0) {
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          float v[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int i = 2 * k + e;
+            const int bp = j * SBITS;
+            const int dw = bp >> 5, off = bp & 31;
+            uint32_t sym = u[i][dw] >> off;
+            if (off + SBITS > 32) sym |= u[i][dw + 1] << (32 - off);
+            const float s = static_cast<float>(sym & mask);
+            if (half == 0) {
+              v[e] = fma3(s, ks[i], kz[i]);
+            } else {
+              v[e] = fma3(s, vmeta[0][gi][tt0 + j], vmeta[1][gi][tt0 + j]);
+            }
+          }
+          o[k] = out_bits2<BF16>(v[0], v[1]);
+        }
+        uint16_t* dst = second ? dst_b + (jj - jsplit) * p.C : dst_a + jj * p.C;
+        const u32x4 x = {o[0], o[1], o[2], o[3]};
+        __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dst));
+      }
+    }
+  }
+}
+
+// Sink tokens [0, sink) of both halves: 8 channels per thread (C % 8 == 0).
+template <bool BF16, bool META_HALF>
+__global__ __launch_bounds__(kDqThreads) void kivi_sink_kernel(KiviParams p) {
+  const int64_t G = p.C >> 3;
+  const int64_t total = 2 * p.sink * G;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kDqThreads + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kDqThreads) {
+    const int64_t g = i % G;
+    const int64_t r = i / G;
+    const int64_t t = r % p.sink;
+    const int half = static_cast<int>(r / p.sink);
+    const int64_t blk = t / p.bs;
+    const int64_t row = kivi_row(p, half, blk, t - blk * p.bs);
+    if (row < 0) continue;
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t e = t * p.C + g * 8 + 2 * k;
+      o[k] = out_bits<BF16>(load_meta<META_HALF>(p.half[half].sink, e)) |
+             (out_bits<BF16>(load_meta<META_HALF>(p.half[half].sink, e + 1)) << 16);
+    }
+    const u32x4 x = {o[0], o[1], o[2], o[3]};
+    __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(p.cache + row * p.C + g * 8));
+  }
+}
+
+// One thread per destination element of both halves: any shape, any group,
+// any alignment (the reference kernel's mapping).
+template <bool BF16, bool META_HALF>
+__global__ __launch_bounds__(kDqThreads) void kivi_generic_kernel(KiviParams p, int32_t bits,
+                                                                  int32_t nib3,
+                                                                  int64_t block_count) {
+  const int64_t per_half = p.bs * p.C;
+  const int64_t total = block_count * 2 * per_half;
+  const int64_t tokens = p.sink + p.body;
+  for (int64_t idx = static_cast<int64_t>(blockIdx.x) * kDqThreads + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * kDqThreads) {
+    const int64_t lb = idx / (2 * per_half);
+    const int64_t r0 = idx - lb * 2 * per_half;
+    const int half = static_cast<int>(r0 / per_half);
+    const int64_t r = r0 - half * per_half;
+    const int64_t off = r / p.C;
+    const int64_t ch = r - off * p.C;
+    const int64_t t = lb * p.bs + off;
+    if (t >= tokens) continue;
+    const int64_t row = kivi_row(p, half, lb, off);
+    if (row < 0) continue;
+    const KiviHalf& hs = p.half[half];
+    float v;
+    if (t < p.sink) {
+      v = load_meta<META_HALF>(hs.sink, t * p.C + ch);
+    } else {
+      const int64_t bt = t - p.sink;
+      const int64_t h = ch / p.D, d = ch - h * p.D;
+      const int64_t idx_s = (half == 0 ? d * p.H + h : h * p.D + d) * p.body + bt;
+      uint32_t sv;
+      if (nib3) {
+        const int64_t o = (hs.bit_bias >> 3) + (idx_s >> 1);
+        const uint32_t w = static_cast<uint32_t>(load_window<1>(
+            ByteStream{reinterpret_cast<const uint32_t*>(hs.sbase), hs.sbytes, 0}, o));
+        sv = (w >> (4 * (idx_s & 1))) & 0x7u;
+      } else {
+        const int64_t bit = hs.bit_bias + idx_s * bits;
+        const uint64_t w = load_window<2>(
+            ByteStream{reinterpret_cast<const uint32_t*>(hs.sbase), hs.sbytes, 0}, bit >> 3);
+        sv = static_cast<uint32_t>(w >> (bit & 7)) & ((1u << bits) - 1u);
+      }
+      int64_t mi;
+      if (half == 0) {
+        mi = (bt / p.group) * p.C + ch;
+      } else {
+        mi = bt * p.vgroups + ch / p.group;
+      }
+      v = __builtin_fmaf(static_cast<float>(sv), load_meta<META_HALF>(hs.scale, mi),
+                         load_meta<META_HALF>(hs.zero, mi));
+    }
+    p.cache[row * p.C + ch] = static_cast<uint16_t>(out_bits<BF16>(v));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host helpers
 // ---------------------------------------------------------------------------
 
@@ -323,6 +612,34 @@ int launch_cachegen_cache(const CacheGenCacheParams& p, int bits, bool bf16, boo
   }
 #undef ORIGAMI_CG_CASE
   return check_launch("cachegen_cache_kernel");
+}
+
+template <int SBITS, bool NIB3, bool BF16, bool META_HALF>
+int launch_kivi_rows(const KiviParams& params, int64_t body, hipStream_t stream) {
+  constexpr int64_t tile_t = 8 * kivi_lane_tokens(SBITS);
+  const int64_t nst = (body + tile_t - 1) / tile_t;
+  ORIGAMI_REQUIRE(params.nct * nst <= INT32_MAX, "KIVI layer exceeds the launch grid");
+  const dim3 grid(static_cast<unsigned>(params.nct * nst), 2);
+  hipLaunchKernelGGL((kivi_cache_kernel<SBITS, NIB3, BF16, META_HALF>), grid, dim3(kKiviThreads),
+                     0, stream, params);
+  return check_launch("kivi_cache_kernel");
+}
+
+template <bool BF16, bool META_HALF>
+int launch_kivi_cache(const KiviParams& p, int64_t body, int sbits, bool nib3,
+                      hipStream_t stream) {
+  if (nib3) return launch_kivi_rows<4, true, BF16, META_HALF>(p, body, stream);
+  switch (sbits) {
+    case 1: return launch_kivi_rows<1, false, BF16, META_HALF>(p, body, stream);
+    case 2: return launch_kivi_rows<2, false, BF16, META_HALF>(p, body, stream);
+    case 3: return launch_kivi_rows<3, false, BF16, META_HALF>(p, body, stream);
+    case 4: return launch_kivi_rows<4, false, BF16, META_HALF>(p, body, stream);
+    case 5: return launch_kivi_rows<5, false, BF16, META_HALF>(p, body, stream);
+    case 6: return launch_kivi_rows<6, false, BF16, META_HALF>(p, body, stream);
+    case 7: return launch_kivi_rows<7, false, BF16, META_HALF>(p, body, stream);
+    case 8: return launch_kivi_rows<8, false, BF16, META_HALF>(p, body, stream);
+    default: return check_bits(sbits);
+  }
 }
 
 }  // namespace
@@ -491,6 +808,126 @@ int origami_cachegen_unpack_dequantize(const uint8_t* bytestream, int64_t bytest
     if (int rc = check_launch("cachegen_dense_kernel")) return rc;
   }
   return ORIGAMI_OK;
+}
+
+int origami_kivi_dequantize_to_kv_cache(
+    const uint8_t* bytestream, int64_t bytestream_bytes, int64_t key_offset, int64_t key_bytes,
+    int64_t value_offset, int64_t value_bytes, int64_t bits, int64_t symbol_packing,
+    int64_t group_size, int64_t sink_tokens, const void* key_scale, const void* key_zero,
+    const void* value_scale, const void* value_zero, const void* key_sink,
+    const void* value_sink, const int64_t* meta_counts, int64_t meta_dtype, void* kv_cache,
+    int64_t cache_dtype, int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+    const int64_t* block_ids, int64_t block_count, int64_t tokens, int64_t heads,
+    int64_t head_dim, origami_stream_t stream) {
+  ORIGAMI_REQUIRE(cache_dtype == ORIGAMI_DTYPE_FLOAT16 || cache_dtype == ORIGAMI_DTYPE_BFLOAT16,
+                  "kv_cache must be float16 or bfloat16");
+  ORIGAMI_REQUIRE(meta_dtype == ORIGAMI_DTYPE_FLOAT16 || meta_dtype == ORIGAMI_DTYPE_FLOAT32,
+                  "KIVI metadata tensors must be float16 or float32");
+  if (int rc = check_bits(bits)) return rc;
+  ORIGAMI_REQUIRE(symbol_packing == ORIGAMI_KIVI_PACKED_LSB ||
+                      symbol_packing == ORIGAMI_KIVI_NIBBLE3,
+                  "unknown KIVI symbol packing");
+  ORIGAMI_REQUIRE(group_size > 0, "KIVI group_size must be positive");
+  ORIGAMI_REQUIRE(sink_tokens >= 0 && sink_tokens <= tokens,
+                  "KIVI sink_tokens must be in [0, tokens]");
+  ORIGAMI_REQUIRE(tokens > 0 && heads > 0 && head_dim > 0,
+                  "tokens, heads, and head_dim must be positive");
+  ORIGAMI_REQUIRE(key_offset >= 0 && key_bytes >= 0 && value_offset >= 0 && value_bytes >= 0,
+                  "invalid KIVI stream offsets");
+  ORIGAMI_REQUIRE(key_offset + key_bytes <= bytestream_bytes &&
+                      value_offset + value_bytes <= bytestream_bytes,
+                  "KIVI stream ranges exceed bytestream length");
+  const int64_t body = tokens - sink_tokens;
+  const int64_t C = heads * head_dim;
+  ORIGAMI_REQUIRE(C <= (int64_t(1) << 24), "heads * head_dim exceeds 2^24");
+  const int64_t key_groups = (body + group_size - 1) / group_size;
+  const int64_t value_groups = (C + group_size - 1) / group_size;
+  ORIGAMI_REQUIRE(meta_counts[0] >= key_groups * C && meta_counts[1] >= key_groups * C,
+                  "KIVI key metadata is too small");
+  ORIGAMI_REQUIRE(meta_counts[2] >= body * value_groups && meta_counts[3] >= body * value_groups,
+                  "KIVI value metadata is too small");
+  ORIGAMI_REQUIRE(meta_counts[4] >= sink_tokens * C && meta_counts[5] >= sink_tokens * C,
+                  "KIVI sink metadata is too small");
+  const size_t esize = meta_dtype == ORIGAMI_DTYPE_FLOAT16 ? 2 : 4;
+  const void* metas[6] = {key_scale, key_zero, value_scale, value_zero, key_sink, value_sink};
+  for (const void* m : metas) {
+    ORIGAMI_REQUIRE(reinterpret_cast<uintptr_t>(m) % esize == 0,
+                    "KIVI metadata must be aligned to its element size");
+  }
+  ORIGAMI_REQUIRE(block_size > 0, "kv_cache block size must be positive");
+  ORIGAMI_REQUIRE(num_blocks > 0, "kv_cache must hold at least one block");
+  ORIGAMI_REQUIRE(block_count > 0, "block_ids must be non-empty");
+  ORIGAMI_REQUIRE(tokens <= block_count * block_size, "tokens exceed destination block capacity");
+  KiviParams p{};
+  if (int rc = cache_geometry(cache_layout, num_blocks, block_size, &p.blk_stride,
+                              &p.half_stride))
+    return rc;
+  const int64_t offs[2] = {key_offset, value_offset};
+  const int64_t lens[2] = {key_bytes, value_bytes};
+  for (int half = 0; half < 2; ++half) {
+    const ByteStream bs = make_stream(bytestream + offs[half], lens[half]);
+    p.half[half].sbase = reinterpret_cast<const uint8_t*>(bs.base);
+    p.half[half].sbytes = bs.bytes;
+    p.half[half].bit_bias = static_cast<int64_t>(bs.bias) * 8;
+    p.half[half].scale = half == 0 ? key_scale : value_scale;
+    p.half[half].zero = half == 0 ? key_zero : value_zero;
+    p.half[half].sink = half == 0 ? key_sink : value_sink;
+  }
+  p.cache = static_cast<uint16_t*>(kv_cache);
+  p.block_ids = block_ids;
+  p.num_blocks = num_blocks;
+  p.bs = block_size;
+  p.sink = sink_tokens;
+  p.body = body;
+  p.C = C;
+  p.H = heads;
+  p.D = head_dim;
+  p.group = group_size;
+  p.vgroups = value_groups;
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool bf16 = cache_dtype == ORIGAMI_DTYPE_BFLOAT16;
+  const bool mhalf = meta_dtype == ORIGAMI_DTYPE_FLOAT16;
+  const bool nib3 = symbol_packing == ORIGAMI_KIVI_NIBBLE3 && bits == 3;
+  const int sbits = nib3 ? 4 : static_cast<int>(bits);
+
+  const bool rows = C % 8 == 0 && head_dim % 8 == 0 && group_size % 16 == 0 &&
+                    block_size >= 16 && aligned16(kv_cache);
+  if (!rows) {
+    const dim3 grid(grid_for(block_count * 2 * block_size * C, kDqThreads, 65536));
+#define ORIGAMI_KIVI_GENERIC(BF, MH)                                                          \
+  hipLaunchKernelGGL((kivi_generic_kernel<BF, MH>), grid, dim3(kDqThreads), 0, st, p,          \
+                     static_cast<int32_t>(bits), static_cast<int32_t>(nib3), block_count)
+    if (bf16) {
+      if (mhalf) ORIGAMI_KIVI_GENERIC(true, true); else ORIGAMI_KIVI_GENERIC(true, false);
+    } else {
+      if (mhalf) ORIGAMI_KIVI_GENERIC(false, true); else ORIGAMI_KIVI_GENERIC(false, false);
+    }
+#undef ORIGAMI_KIVI_GENERIC
+    return check_launch("kivi_generic_kernel");
+  }
+  if (sink_tokens > 0) {
+    const dim3 grid(grid_for(2 * sink_tokens * (C / 8), kDqThreads, 65536));
+    if (bf16) {
+      if (mhalf)
+        hipLaunchKernelGGL((kivi_sink_kernel<true, true>), grid, dim3(kDqThreads), 0, st, p);
+      else
+        hipLaunchKernelGGL((kivi_sink_kernel<true, false>), grid, dim3(kDqThreads), 0, st, p);
+    } else {
+      if (mhalf)
+        hipLaunchKernelGGL((kivi_sink_kernel<false, true>), grid, dim3(kDqThreads), 0, st, p);
+      else
+        hipLaunchKernelGGL((kivi_sink_kernel<false, false>), grid, dim3(kDqThreads), 0, st, p);
+    }
+    if (int rc = check_launch("kivi_sink_kernel")) return rc;
+  }
+  if (body <= 0) return ORIGAMI_OK;
+  p.nct = static_cast<int32_t>((C + kKiviTileChannels - 1) / kKiviTileChannels);
+  if (bf16) {
+    return mhalf ? launch_kivi_cache<true, true>(p, body, sbits, nib3, st)
+                 : launch_kivi_cache<true, false>(p, body, sbits, nib3, st);
+  }
+  return mhalf ? launch_kivi_cache<false, true>(p, body, sbits, nib3, st)
+               : launch_kivi_cache<false, false>(p, body, sbits, nib3, st);
 }
 
 }  // extern "C"

@@ -33,6 +33,44 @@ inline unsigned grid_for(int64_t work, int64_t per_block, int64_t cap) {
   return static_cast<unsigned>(g);
 }
 
+// ---------------------------------------------------------------------------
+// Device helpers shared by the row kernels
+// ---------------------------------------------------------------------------
+
+// The dword at byte offset `byte` (a multiple of 4) of a 4-byte aligned
+// buffer of `nbytes` readable bytes; bytes at or past nbytes read as 0.  A
+// dword is read only when it holds at least one readable byte, so the read
+// never leaves the pages the buffer occupies; its unreadable bytes are masked.
+__device__ __forceinline__ uint32_t load_dword_guarded(const uint8_t* base, int64_t byte,
+                                                       int64_t nbytes) {
+  const int64_t avail = nbytes - byte;
+  if (avail <= 0) return 0;
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(base + byte);
+  return avail >= 4 ? w : (w & ((1u << (8 * avail)) - 1u));
+}
+
+// Spreads 16 b-bit symbols packed LSB-first in u[] into 16 bytes
+// (byte j of the result, dword j / 4, is symbol j).
+template <int BITS>
+__device__ __forceinline__ void expand16(const uint32_t* u, uint32_t (&out)[4]) {
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = u[i];
+  } else {
+    constexpr uint32_t mask = (1u << BITS) - 1u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int bp = j * BITS;
+      const int dw = bp >> 5, off = bp & 31;
+      uint32_t s = u[dw] >> off;
+      if (off + BITS > 32) s |= u[dw + 1] << (32 - off);
+      out[j >> 2] |= (s & mask) << (8 * (j & 3));
+    }
+  }
+}
+
 }  // namespace origami_internal
 
 #define ORIGAMI_REQUIRE(cond, msg)                                              \

@@ -410,37 +410,6 @@ __device__ __forceinline__ void transpose16(const uint32_t (&in)[16][4],
   }
 }
 
-__device__ __forceinline__ uint32_t load_dword_guarded(const uint8_t* base, int64_t byte,
-                                                       int64_t nbytes) {
-  if (byte + 4 <= nbytes) return *reinterpret_cast<const uint32_t*>(base + byte);
-  uint32_t w = 0;
-#pragma unroll
-  for (int b = 0; b < 4; ++b)
-    if (byte + b < nbytes) w |= static_cast<uint32_t>(base[byte + b]) << (8 * b);
-  return w;
-}
-
-// Spreads 16 b-bit symbols packed LSB-first in u[] into 16 bytes.
-template <int BITS>
-__device__ __forceinline__ void expand16(const uint32_t* u, uint32_t (&out)[4]) {
-  if constexpr (BITS == 8) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = u[i];
-  } else {
-    constexpr uint32_t mask = (1u << BITS) - 1u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = 0;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int bp = j * BITS;
-      const int dw = bp >> 5, off = bp & 31;
-      uint32_t s = u[dw] >> off;
-      if (off + BITS > 32) s |= u[dw + 1] << (32 - off);
-      out[j >> 2] |= (s & mask) << (8 * (j & 3));
-    }
-  }
-}
-
 // Packs 16 bytes (symbols, masked to b bits) LSB-first into u[].
 template <int BITS>
 __device__ __forceinline__ void compress16(const uint32_t (&in)[4], uint32_t* u) {

@@ -1,8 +1,8 @@
 """GPU layout path: Python front end of liborigami_layout.so.
 
 Mirrors lossless/native_gpu.py of the reference (load_bitpack_cuda_extension,
-available, unpack_canonical_storage_chunks, cachegen_unpack_dequantize*;
-native_gpu.py:35-215) and adds the pieces the reference lacks: the pack, the
+available, unpack_canonical_storage_chunks, cachegen_unpack_dequantize*,
+kivi_dequantize_to_kv_cache; native_gpu.py:35-261) and adds the pieces the reference lacks: the pack, the
 fused unpack+scatter into the paged KV cache and the fused gather+pack from
 it.
 
@@ -329,7 +329,7 @@ def gather_kv_blocks(kv_cache: torch.Tensor, block_ids: torch.Tensor,
 
 
 # ---------------------------------------------------------------------------
-# Fused dequantize paths (CacheGen)
+# Fused dequantize paths (CacheGen, KIVI)
 # ---------------------------------------------------------------------------
 
 _DTYPE_CODES = {
@@ -449,6 +449,58 @@ def cachegen_unpack_dequantize(
     return out
 
 
+_KIVI_PACKING = {"lsb": _native.KIVI_PACKED_LSB, "kivi": _native.KIVI_NIBBLE3}
+
+
+def kivi_dequantize_to_kv_cache(
+    bytestream: torch.Tensor, *, key_offset: int, key_bytes: int, value_offset: int,
+    value_bytes: int, bits: int, group_size: int, sink_tokens: int, key_scale: torch.Tensor,
+    key_zero: torch.Tensor, value_scale: torch.Tensor, value_zero: torch.Tensor,
+    key_sink: torch.Tensor, value_sink: torch.Tensor, kv_cache: torch.Tensor,
+    block_ids: torch.Tensor, tokens: int, heads: int, head_dim: int,
+    symbol_packing: str = "lsb",
+) -> None:
+    """KIVI fused restore into the paged cache (native_gpu.py:218-261,
+    bitpack_layout_cuda.cpp:583-714): sink tokens are copied, body tokens
+    dequantized with per-channel key groups and per-token value groups, all
+    written through the block table.  symbol_packing "lsb" reads b-bit
+    symbols LSB-first, as the reference kernel does; "kivi" reads KIVI's own
+    container (kivi_adapter.py:28-54), whose 3-bit symbols sit one per
+    nibble."""
+    flat = bytestream.reshape(-1)
+    if not flat.is_contiguous():
+        flat = flat.contiguous()
+    _require_cuda(flat, "bytestream")
+    if flat.dtype != torch.uint8:
+        raise RuntimeError("bytestream must be uint8")
+    _require_cuda(kv_cache, "kv_cache")
+    if kv_cache.dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError("kv_cache must be float16 or bfloat16")
+    metas = [t.contiguous() for t in (key_scale, key_zero, value_scale, value_zero, key_sink,
+                                      value_sink)]
+    for t, name in zip(metas, ("key_scale", "key_zero", "value_scale", "value_zero", "key_sink",
+                               "value_sink")):
+        _require_cuda(t, name)
+    if any(t.dtype != metas[0].dtype for t in metas):
+        raise RuntimeError("KIVI metadata tensors must have the same dtype")
+    if metas[0].dtype not in (torch.float16, torch.float32):
+        raise RuntimeError("KIVI metadata tensors must be float16 or float32")
+    if symbol_packing not in _KIVI_PACKING:
+        raise ValueError(f"symbol_packing must be one of {sorted(_KIVI_PACKING)}")
+    counts = _native.i64_array([t.numel() for t in metas])
+    ids = block_ids.to(device=kv_cache.device, dtype=torch.int64).contiguous()
+    code, nb, bs = dequant_cache_geometry(kv_cache, heads, head_dim)
+    with torch.cuda.device(kv_cache.device):
+        _native.call(
+            "origami_kivi_dequantize_to_kv_cache",
+            flat.data_ptr(), flat.numel(), int(key_offset), int(key_bytes), int(value_offset),
+            int(value_bytes), int(bits), _KIVI_PACKING[symbol_packing], int(group_size),
+            int(sink_tokens), *[t.data_ptr() for t in metas], _native.host_ptr(counts),
+            _DTYPE_CODES[metas[0].dtype], kv_cache.data_ptr(), _DTYPE_CODES[kv_cache.dtype], code,
+            nb, bs, ids.data_ptr(), ids.numel(), int(tokens), int(heads), int(head_dim),
+            _stream_handle(kv_cache.device))
+
+
 # ---------------------------------------------------------------------------
 # Reference extension surface (origami_bitpack_cuda_v6, cpp:894-903)
 # ---------------------------------------------------------------------------
@@ -510,8 +562,24 @@ class _Extension:
             head_dim=head_dim)
 
     @staticmethod
-    def kivi_dequantize_to_kv_cache_cuda(*args: Any, **kwargs: Any) -> None:
-        raise NotImplementedError("KIVI dequantize-to-cache is not part of this build yet")
+    def kivi_dequantize_to_kv_cache_cuda(
+        bytestream: torch.Tensor, key_offset: int, key_bytes: int, value_offset: int,
+        value_bytes: int, bits: int, group_size: int, sink_tokens: int, key_scale: torch.Tensor,
+        key_zero: torch.Tensor, value_scale: torch.Tensor, value_zero: torch.Tensor,
+        key_sink: torch.Tensor, value_sink: torch.Tensor, kv_cache: torch.Tensor,
+        block_ids: torch.Tensor, tokens: int, heads: int, head_dim: int,
+    ) -> None:
+        """Signature of bitpack_layout_cuda.cpp:583-602 (LSB-first symbols)."""
+        for t, name in ((bytestream, "bytestream"), (block_ids, "block_ids")):
+            _require_cuda(t, name)
+        if block_ids.dtype != torch.int64:
+            raise RuntimeError("block_ids must be int64")
+        kivi_dequantize_to_kv_cache(
+            bytestream, key_offset=key_offset, key_bytes=key_bytes, value_offset=value_offset,
+            value_bytes=value_bytes, bits=bits, group_size=group_size, sink_tokens=sink_tokens,
+            key_scale=key_scale, key_zero=key_zero, value_scale=value_scale,
+            value_zero=value_zero, key_sink=key_sink, value_sink=value_sink, kv_cache=kv_cache,
+            block_ids=block_ids, tokens=tokens, heads=heads, head_dim=head_dim)
 
     @staticmethod
     def cachegen_unpack_dequantize_cuda(
@@ -547,5 +615,5 @@ __all__ = [
     "block_ids_tensor", "unpack_to_kv_cache", "pack_from_kv_cache", "scatter_kv_blocks",
     "gather_kv_blocks", "kv_symbol_layout", "CACHE_KV_FIRST", "CACHE_BLOCKS_FIRST",
     "cachegen_unpack_dequantize_to_kv_cache", "cachegen_unpack_dequantize",
-    "dequant_cache_geometry",
+    "kivi_dequantize_to_kv_cache", "dequant_cache_geometry",
 ]

@@ -1,5 +1,5 @@
-"""Parity of the HIP CacheGen dequantize kernels (liborigami_layout.so) with
-the CPU oracle (oracle/dequant_oracle.c).
+"""Parity of the HIP CacheGen and KIVI dequantize kernels
+(liborigami_layout.so) with the CPU oracle (oracle/dequant_oracle.c).
 
 Comparisons are bit-exact on the float16 / bfloat16 bits.  The one case with
 bins = 2 (centre 0, so quotients are NaN or infinite) compares NaN positions
@@ -8,6 +8,10 @@ cache layouts, float16 / float32 maxima, float16 / bfloat16 caches, the
 row kernel (C % 8 == 0) and the element kernel (C % 8 != 0 or an unaligned
 cache), unaligned and short streams, skipped block ids, untouched tail
 tokens, and one full Llama-3-8B layer (32768 tokens, 8 KV heads x 128).
+KIVI cases cover bits 1..8 LSB-first and KIVI's 3-bit nibble container,
+sink tokens, key/value groups, the row kernel and the element kernel, partial
+token and channel tiles, blocks that split a lane's 16 tokens, and a full
+Llama-3-8B layer.
 """
 import numpy as np
 import pytest
@@ -15,7 +19,7 @@ import torch
 
 from oracle import oracle
 from origami_amd.lossless import native_gpu
-from tests import bitref
+from tests import bitref, dqref
 
 pytestmark = pytest.mark.gpu
 
@@ -226,3 +230,176 @@ def test_cachegen_errors(cuda_device):
     with pytest.raises(RuntimeError, match="head shape mismatch"):
         native_gpu.cachegen_unpack_dequantize_to_kv_cache(s, **{**kw, "kv_cache": cache,
                                                                 "head_dim": 8})
+
+
+# ---------------------------------------------------------------------------
+# KIVI
+# ---------------------------------------------------------------------------
+
+def _kivi_case(rng, tokens, sink, heads, head_dim, bits, nibble3, group, meta_dtype, gap=1,
+               short_value=0):
+    C = heads * head_dim
+    body = tokens - sink
+    kq = rng.integers(0, 1 << bits, body * C, dtype=np.uint8).reshape(body, C)
+    vq = rng.integers(0, 1 << bits, body * C, dtype=np.uint8).reshape(body, C)
+    korder = dqref.kivi_key_order(kq, heads, head_dim)
+    vorder = dqref.kivi_value_order(vq, heads, head_dim)
+    if nibble3:
+        ks, vs = dqref.kivi_pack(korder, 3), dqref.kivi_pack(vorder, 3)
+    else:
+        ks, vs = bitref.bits_pack(korder, bits), bitref.bits_pack(vorder, bits)
+    stream = np.concatenate([rng.integers(0, 256, gap, dtype=np.uint8), ks,
+                             rng.integers(0, 256, gap, dtype=np.uint8), vs])
+    kg = (body + group - 1) // group
+    vg = (C + group - 1) // group
+    meta = [(rng.random(kg * C) * 0.5 + 0.01).astype(meta_dtype),
+            rng.standard_normal(kg * C).astype(meta_dtype),
+            (rng.random(body * vg) * 0.5 + 0.01).astype(meta_dtype),
+            rng.standard_normal(body * vg).astype(meta_dtype),
+            rng.standard_normal(sink * C).astype(meta_dtype),
+            rng.standard_normal(sink * C).astype(meta_dtype)]
+    return stream, gap, ks.size, 2 * gap + ks.size, vs.size - short_value, meta
+
+
+def _kivi_run_both(dev, rng, *, tokens, sink, heads, head_dim, bits, nibble3=False, group,
+                   bs, nb, ids, out_dtype, meta_dtype, blocks_first, gap=1, short_value=0,
+                   cache_offset=0):
+    stream, koff, kb, voff, vb, meta = _kivi_case(rng, tokens, sink, heads, head_dim, bits,
+                                                  nibble3, group, meta_dtype, gap, short_value)
+    shape = (nb, 2, bs, heads, head_dim) if blocks_first else (2, nb, bs, heads, head_dim)
+    n = int(np.prod(shape))
+    init = rng.integers(-(1 << 14), 1 << 14, n + cache_offset, dtype=np.int16)
+    cache = torch.from_numpy(init).to(dev).view(out_dtype)[cache_offset:].view(shape)
+    expect = init[cache_offset:].view(np.uint16).reshape(shape).copy()
+    oracle.kivi_to_kv_cache(stream, koff, kb, voff, vb, bits, nibble3, group, sink, *meta, expect,
+                            out_dtype == torch.bfloat16, blocks_first, ids, tokens, heads,
+                            head_dim)
+    dm = [torch.from_numpy(m).to(dev) for m in meta]
+    native_gpu.kivi_dequantize_to_kv_cache(
+        torch.from_numpy(stream).to(dev), key_offset=koff, key_bytes=kb, value_offset=voff,
+        value_bytes=vb, bits=bits, group_size=group, sink_tokens=sink, key_scale=dm[0],
+        key_zero=dm[1], value_scale=dm[2], value_zero=dm[3], key_sink=dm[4], value_sink=dm[5],
+        kv_cache=cache, block_ids=torch.tensor(ids, dtype=torch.int64, device=dev),
+        tokens=tokens, heads=heads, head_dim=head_dim,
+        symbol_packing="kivi" if nibble3 else "lsb")
+    torch.cuda.synchronize(dev)
+    return _bits16(cache), expect
+
+
+KIVI_BITS = [(2, False), (3, True), (3, False), (4, False), (8, False), (1, False), (5, False),
+             (6, False), (7, False)]
+
+
+@pytest.mark.parametrize("blocks_first", [False, True])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("meta_dtype", [np.float16, np.float32])
+@pytest.mark.parametrize("kb", range(len(KIVI_BITS)))
+def test_kivi_row_kernel(cuda_device, kb, meta_dtype, out_dtype, blocks_first):
+    bits, nibble3 = KIVI_BITS[kb]
+    rng = np.random.default_rng(300 + kb)
+    # body = 600 - 24 = 576 tokens: one full 512-token tile and a partial one;
+    # C = 128: two channel tiles; group 32.
+    ids = rng.permutation(45)[:38].tolist()
+    ids[5] = -1
+    got, exp = _kivi_run_both(cuda_device, rng, tokens=600, sink=24, heads=2, head_dim=64,
+                              bits=bits, nibble3=nibble3, group=32, bs=16, nb=45, ids=ids,
+                              out_dtype=out_dtype, meta_dtype=meta_dtype,
+                              blocks_first=blocks_first)
+    assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("case", ["group16", "group64_sink128", "no_sink", "generic_group",
+                                  "generic_head_dim", "unaligned_cache", "short_value_stream",
+                                  "c_partial_tile", "block_size_7", "all_sink"])
+def test_kivi_shapes(cuda_device, case):
+    rng = np.random.default_rng(sum(map(ord, case)))
+    kw = dict(tokens=300, sink=20, heads=4, head_dim=16, bits=2, group=32, bs=16, nb=40,
+              ids=list(range(39, 20, -1)), out_dtype=torch.bfloat16, meta_dtype=np.float16,
+              blocks_first=False)
+    if case == "group16":
+        kw.update(group=16)
+    elif case == "group64_sink128":
+        kw.update(tokens=1000, sink=128, group=64, ids=list(range(63)), nb=70)
+    elif case == "no_sink":
+        kw.update(sink=0)
+    elif case == "generic_group":                # group % 16 != 0: element kernel
+        kw.update(group=5, bits=3, nibble3=True)
+    elif case == "generic_head_dim":             # head_dim % 8 != 0: element kernel
+        kw.update(heads=3, head_dim=12, bits=4)
+    elif case == "unaligned_cache":
+        kw.update(cache_offset=1)
+    elif case == "short_value_stream":           # symbols past value_bytes read 0
+        kw.update(short_value=9)
+    elif case == "c_partial_tile":               # C = 96: the second channel tile is partial
+        kw.update(heads=3, head_dim=32, bits=4)
+    elif case == "block_size_7":                 # lane tokens straddle blocks
+        kw.update(bs=7, nb=50, ids=list(range(49, 6, -1)))
+    elif case == "all_sink":
+        kw.update(tokens=40, sink=40, ids=[3, 1, 2])
+    got, exp = _kivi_run_both(cuda_device, rng, **kw)
+    assert np.array_equal(got, exp)
+
+
+def test_kivi_llama3_8b_layer(cuda_device):
+    """A full layer at the Llama-3-8B geometry: 32768 tokens, 128 sink tokens,
+    group 32, 2-bit KIVI, permuted block table."""
+    rng = np.random.default_rng(9)
+    tokens, bs = 32768, 16
+    nb = tokens // bs + 32
+    ids = rng.permutation(nb)[: tokens // bs].tolist()
+    got, exp = _kivi_run_both(cuda_device, rng, tokens=tokens, sink=128, heads=8, head_dim=128,
+                              bits=2, group=32, bs=bs, nb=nb, ids=ids, out_dtype=torch.bfloat16,
+                              meta_dtype=np.float16, blocks_first=False, gap=0)
+    assert np.array_equal(got, exp)
+
+
+def test_kivi_extension_surface_and_errors(cuda_device):
+    ext = native_gpu.load_bitpack_cuda_extension()
+    dev = cuda_device
+    rng = np.random.default_rng(4)
+    tokens, sink, heads, head_dim, group = 64, 16, 2, 16, 16
+    stream, koff, kb, voff, vb, meta = _kivi_case(rng, tokens, sink, heads, head_dim, 4, False,
+                                                  group, np.float16)
+    cache = torch.zeros((2, 5, 16, heads, head_dim), dtype=torch.float16, device=dev)
+    expect = np.zeros(cache.shape, np.uint16)
+    oracle.kivi_to_kv_cache(stream, koff, kb, voff, vb, 4, False, group, sink, *meta, expect,
+                            False, False, [4, 0, 3, 1], tokens, heads, head_dim)
+    dm = [torch.from_numpy(m).to(dev) for m in meta]
+    ids = torch.tensor([4, 0, 3, 1], dtype=torch.int64, device=dev)
+    s = torch.from_numpy(stream).to(dev)
+    ext.kivi_dequantize_to_kv_cache_cuda(s, koff, kb, voff, vb, 4, group, sink, *dm, cache, ids,
+                                         tokens, heads, head_dim)
+    assert np.array_equal(_bits16(cache), expect)
+    args = [s, koff, kb, voff, vb, 4, group, sink, *dm, cache, ids, tokens, heads, head_dim]
+    bad = list(args)
+    bad[6] = 0
+    with pytest.raises(RuntimeError, match="group_size must be positive"):
+        ext.kivi_dequantize_to_kv_cache_cuda(*bad)
+    bad = list(args)
+    bad[7] = tokens + 1
+    with pytest.raises(RuntimeError, match="sink_tokens must be in"):
+        ext.kivi_dequantize_to_kv_cache_cuda(*bad)
+    bad = list(args)
+    bad[8] = dm[0][:-1]
+    with pytest.raises(RuntimeError, match="key metadata is too small"):
+        ext.kivi_dequantize_to_kv_cache_cuda(*bad)
+    bad = list(args)
+    bad[10] = dm[2][:-1]
+    with pytest.raises(RuntimeError, match="value metadata is too small"):
+        ext.kivi_dequantize_to_kv_cache_cuda(*bad)
+    bad = list(args)
+    bad[13] = dm[5][:-1]
+    with pytest.raises(RuntimeError, match="sink metadata is too small"):
+        ext.kivi_dequantize_to_kv_cache_cuda(*bad)
+    bad = list(args)
+    bad[9] = dm[1].float()
+    with pytest.raises(RuntimeError, match="same dtype"):
+        ext.kivi_dequantize_to_kv_cache_cuda(*bad)
+    bad = list(args)
+    bad[5] = 9
+    with pytest.raises(RuntimeError, match="supports only 1..8"):
+        ext.kivi_dequantize_to_kv_cache_cuda(*bad)
+    bad = list(args)
+    bad[4] = len(stream)
+    with pytest.raises(RuntimeError, match="exceed bytestream length"):
+        ext.kivi_dequantize_to_kv_cache_cuda(*bad)
