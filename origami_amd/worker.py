@@ -17,8 +17,10 @@ adapter is packed on the GPU straight from the paged cache (fused block gather
 + plane-major pack) and restored through LayerRestorePipeline: decompression
 into pinned staging, H2D on a copy stream, fused unpack + block-table scatter on
 a compute stream, one event per layer.  Payloads in the reference's raw_bytes
-format restore through the same pipeline with a block scatter.  Other
-canonical payloads unpack on the GPU and go through copy_kv_to_hbm.
+format restore through the same pipeline with a block scatter, and CacheGen
+bit-packed and KIVI payloads with their fused unpack + dequantize + scatter
+kernels.  Other canonical payloads unpack on the GPU, dequantize through their
+adapter and go through copy_kv_to_hbm.
 """
 from __future__ import annotations
 
@@ -54,6 +56,8 @@ from origami_amd.restore_pipeline import LayerRestorePipeline
 from origami_amd.store import OrigamiStore
 
 _NATIVE_LAYOUT_KEY = "origami_native_layout"
+# quantized payloads whose restore has a fused HIP dequantize-to-cache path
+_FUSED_DEQUANT_FORMATS = ("cachegen_bitpacked_blob", "kivi_structured_blob")
 
 
 def _layer_index(layer_name: str) -> int:
@@ -215,6 +219,11 @@ class OrigamiConnectorWorker:
             if fmt == "raw_bytes" and kv_cache.is_cuda and self._raw_bytes_scatterable(
                     meta, kv_cache, layout):
                 return self._restore_raw_bytes(layer_payload, layout, kv_cache, block_ids, nb, meta)
+            if fmt in _FUSED_DEQUANT_FORMATS and kv_cache.is_cuda:
+                result = self._restore_fused_dequant(restore, layer_payload, layout, kv_cache,
+                                                     block_ids, nb, meta)
+                if result is not None:
+                    return result
             return self._restore_generic(restore, layer_payload, layout, kv_cache, block_ids)
 
     def _fill_from_chunks(self, layer_payload: LayerPayload, layout: CanonicalLayout):
@@ -265,6 +274,31 @@ class OrigamiConnectorWorker:
         event = pipe.submit(
             self._fill_from_chunks(layer_payload, layout), layout.stream_bytes,
             lambda flat: native_gpu.scatter_kv_blocks(flat, tokens, kv_cache, ids_dev))
+        return _LayerLoadResult(event=event)
+
+    def _restore_fused_dequant(self, restore, layer_payload, layout, kv_cache, block_ids, nb,
+                               meta):
+        """CacheGen bit-packed and KIVI payloads restored whole into whole
+        blocks: the blob goes to the device on the copy stream and one fused
+        unpack + dequantize + paged scatter runs on the compute stream
+        (worker.py:1250-1346 with cachegen_adapter.py:656-819 and
+        kivi_adapter.py:537-683).  None when the payload does not qualify."""
+        can = getattr(self.quantizer, "can_dequantize_to_cache", None)
+        tokens = int(meta.get("token_count", 0) or 0)
+        if can is None or tokens <= 0 or tokens != int(restore.num_tokens):
+            return None
+        if not can(meta, kv_cache, block_ids, tokens=tokens):
+            return None
+        if list(layout.shape[:2]) != [1, 1] or layout.uniform_bits != 8:
+            return None  # the blob must travel as plain bytes
+        needed = -(-tokens // int(kv_cache.shape[2]))
+        ids_dev = native_gpu.block_ids_tensor(block_ids[:needed], kv_cache.device, nb)
+        pipe = self._pipeline(kv_cache.device, layout.stream_bytes)
+        ids_dev.record_stream(pipe.compute_stream)
+        quantizer = self.quantizer
+        event = pipe.submit(
+            self._fill_from_chunks(layer_payload, layout), layout.stream_bytes,
+            lambda flat: quantizer.dequantize_to_cache(flat, meta, kv_cache, ids_dev, tokens))
         return _LayerLoadResult(event=event)
 
     def _restore_generic(self, restore, layer_payload, layout, kv_cache, block_ids):

@@ -74,7 +74,7 @@ def test_adapters_byte_views():
     assert torch.equal(raw.dequantize(r.symbols, r.metadata).view(torch.int16),
                        kv.view(torch.int16))
     with pytest.raises(ValueError):
-        create_quantizer_adapter("cachegen")
+        create_quantizer_adapter("kvquant")
 
 
 def test_normalize_kv_value_shapes():
