@@ -52,8 +52,12 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--no-pipeline", action="store_true")
+    ap.add_argument("--no-dequant", action="store_true",
+                    help="skip the CacheGen / KIVI fused dequantize legs")
     ap.add_argument("--profile-only", action="store_true",
                     help="only the timed restore loop (for rocprofv3 runs)")
+    ap.add_argument("--profile-dequant", action="store_true",
+                    help="with --profile-only: also run the dequantize legs")
     return ap.parse_args()
 
 
@@ -149,6 +153,9 @@ def main() -> int:
     achieved = layer_bytes / (avg_launch_ms * 1e-3) / 1e9
 
     if args.profile_only:
+        if args.profile_dequant:
+            dequant_leg(src_cache, T, bs, torch.zeros_like(dst_caches[0]), dst_ids[0], gen, dev,
+                        args.steps)
         # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain device
         # copy of a known size (256 MiB read + 256 MiB written per launch)
         cal_a = torch.empty(CAL_BYTES, dtype=torch.uint8, device=dev)
@@ -238,12 +245,80 @@ def main() -> int:
         result["pipeline"] = pipeline_leg(streams, layout, T, dst_caches, dst_ids, dev,
                                           avg_launch_ms)
 
+    if not args.no_dequant:
+        result["dequant"] = dequant_leg(src_cache, T, bs, torch.zeros_like(dst_caches[0]),
+                                        dst_ids[0], gen, dev, args.steps)
+
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(streams[0], layout, specs, T, H, C, bs, NB,
                                               dst_ids[0], dst_caches[0], layer_bytes,
                                               args.cpu_reps)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def dequant_leg(src_cache, T, bs, dst_cache, dst_ids, gen, dev, steps):
+    """Fused dequantize-to-cache restores of one layer at the workload's
+    geometry, from payloads the CacheGen and KIVI adapters produce for a
+    synthetic layer: CacheGen quant level 2 at layer 12 (16 bins, 4-bit K and
+    V) and KIVI 2-bit, group 32, 128 sink tokens.  Algorithmic bytes per
+    layer: the K and V symbol streams and the metadata the kernels read, the
+    bf16 cache rows written, and the block table.  Each kernel is timed with
+    events on the stream it is launched on, over `steps` back-to-back
+    launches."""
+    import torch
+
+    from origami_amd.quantization import create_quantizer_adapter
+
+    from origami_amd.synthetic import fill_layer
+
+    nblk = -(-T // bs)
+    ids = torch.randperm(src_cache.shape[1], generator=gen, device=dev)[:nblk].contiguous()
+    fill_layer(src_cache, ids, gen)
+    kv = src_cache[:, ids]
+    H, D = int(src_cache.shape[3]), int(src_cache.shape[4])
+    out_bytes = 2 * T * H * D * 2
+    legs = {}
+    for name, quantizer, cfg in (
+            ("cachegen", "cachegen", {"quant_level": "2"}),
+            ("kivi", "kivi", {"bits": 2, "group_size": 32, "sink_tokens": 128})):
+        a = create_quantizer_adapter(quantizer, cfg)
+        q = a.quantize(kv, layer_group="model.layers.12.self_attn")
+        m, blob = q.metadata, q.symbols
+        if name == "cachegen":
+            read = (m["key_stream_bytes"] + m["value_stream_bytes"]
+                    + 2 * (m["key_max_numel"] + m["value_max_numel"]))
+            kernel = "cachegen_cache_kernel<4, bf16, f16 max>"
+        else:
+            read = (m["key_stream_bytes"] + m["value_stream_bytes"]
+                    + 2 * sum(m[f"{k}_numel"] for k in ("key_scale", "key_zero", "value_scale",
+                                                        "value_zero", "key_sink", "value_sink")))
+            kernel = "kivi_cache_kernel<2, bf16, f16 meta> + kivi_sink_kernel"
+        alg = read + out_bytes + nblk * 8
+
+        def run():
+            a.dequantize_to_cache(blob, m, dst_cache, dst_ids, T)
+
+        for _ in range(3):
+            run()
+        cur = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(cur)
+        for _ in range(steps):
+            run()
+        e1.record(cur)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        gbps = alg / (ms * 1e-3) / 1e9
+        legs[name] = {
+            "kernel": kernel, "bits": [m.get("key_bits", m.get("bits")),
+                                       m.get("value_bits", m.get("bits"))],
+            "per_layer_us": round(ms * 1e3, 2), "algorithmic_bytes_per_layer": int(alg),
+            "gbps": round(gbps, 2), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+        }
+        del q, blob
+    return legs
 
 
 def pipeline_leg(streams, layout, T, dst_caches, dst_ids, dev, kernel_ms):

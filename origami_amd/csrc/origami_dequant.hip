@@ -36,6 +36,7 @@ using namespace origami_internal;
 namespace {
 
 constexpr int kDqThreads = 256;
+constexpr uint32_t kXcds = 8;  // MI355X: 8 accelerator complex dies, one L2 each
 constexpr int64_t kMaxDqGrid = 1 << 20;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -361,6 +362,7 @@ struct KiviParams {
   int64_t C, H, D;
   int64_t group, vgroups;
   int32_t nct;           // workgroups along channels
+  int32_t ntiles;        // row-kernel tiles per half; workgroups past them copy sink rows
 };
 
 // Row index of token t of `half`, or -1 when its block id is outside the cache.
@@ -369,6 +371,28 @@ __device__ __forceinline__ int64_t kivi_row(const KiviParams& p, int half, int64
   const int64_t pid = p.block_ids[blk];
   if (pid < 0 || pid >= p.num_blocks) return -1;
   return pid * p.blk_stride + half * p.half_stride + off;
+}
+
+// Sink tokens [0, sink) of one half, 8 channels per thread (C % 8 == 0):
+// workgroup `wg` of the extra workgroups that follow the row tiles.
+template <bool BF16, bool META_HALF>
+__device__ __forceinline__ void kivi_sink_rows(const KiviParams& p, int half, int64_t wg) {
+  const int64_t G = p.C >> 3;
+  const int64_t i = wg * kKiviThreads + threadIdx.x;
+  if (i >= p.sink * G) return;
+  const int64_t t = i / G, g = i - t * G;
+  const int64_t blk = t / p.bs;
+  const int64_t row = kivi_row(p, half, blk, t - blk * p.bs);
+  if (row < 0) return;
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t e = t * p.C + g * 8 + 2 * k;
+    o[k] = out_bits2<BF16>(load_meta<META_HALF>(p.half[half].sink, e),
+                           load_meta<META_HALF>(p.half[half].sink, e + 1));
+  }
+  const u32x4 x = {o[0], o[1], o[2], o[3]};
+  __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(p.cache + row * p.C + g * 8));
 }
 
 template <int SBITS, bool NIB3, bool BF16, bool META_HALF>
@@ -381,8 +405,18 @@ __global__ __launch_bounds__(kKiviThreads) void kivi_cache_kernel(KiviParams p) 
   const int half = blockIdx.y;
   const KiviHalf& hs = p.half[half];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int ct = static_cast<int>(blockIdx.x % p.nct);
-  const int64_t tile_bt0 = static_cast<int64_t>(blockIdx.x / p.nct) * TILE_T;
+  if (static_cast<int32_t>(blockIdx.x) >= p.ntiles) {
+    kivi_sink_rows<BF16, META_HALF>(p, half, blockIdx.x - p.ntiles);
+    return;
+  }
+  // Workgroups go to the 8 XCDs round-robin and each XCD has its own L2.
+  // Give each XCD a contiguous range of tiles, so that the channel tiles of
+  // one token range (which share their value metadata lines) and the token
+  // tiles that share plane lines meet in the same L2.
+  uint32_t tile = blockIdx.x;
+  if (p.ntiles % kXcds == 0) tile = (tile % kXcds) * (p.ntiles / kXcds) + tile / kXcds;
+  const int ct = static_cast<int>(tile % p.nct);
+  const int64_t tile_bt0 = static_cast<int64_t>(tile / p.nct) * TILE_T;
   const int64_t tile_c0 = static_cast<int64_t>(ct) * kKiviTileChannels;
   const int64_t c0 = tile_c0 + wave * 64 + (lane & 7) * 8;
   const int64_t bt0 = tile_bt0 + (lane >> 3) * LT;
@@ -492,32 +526,6 @@ __global__ __launch_bounds__(kKiviThreads) void kivi_cache_kernel(KiviParams p) 
   }
 }
 
-// Sink tokens [0, sink) of both halves: 8 channels per thread (C % 8 == 0).
-template <bool BF16, bool META_HALF>
-__global__ __launch_bounds__(kDqThreads) void kivi_sink_kernel(KiviParams p) {
-  const int64_t G = p.C >> 3;
-  const int64_t total = 2 * p.sink * G;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kDqThreads + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * kDqThreads) {
-    const int64_t g = i % G;
-    const int64_t r = i / G;
-    const int64_t t = r % p.sink;
-    const int half = static_cast<int>(r / p.sink);
-    const int64_t blk = t / p.bs;
-    const int64_t row = kivi_row(p, half, blk, t - blk * p.bs);
-    if (row < 0) continue;
-    uint32_t o[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int64_t e = t * p.C + g * 8 + 2 * k;
-      o[k] = out_bits<BF16>(load_meta<META_HALF>(p.half[half].sink, e)) |
-             (out_bits<BF16>(load_meta<META_HALF>(p.half[half].sink, e + 1)) << 16);
-    }
-    const u32x4 x = {o[0], o[1], o[2], o[3]};
-    __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(p.cache + row * p.C + g * 8));
-  }
-}
-
 // One thread per destination element of both halves: any shape, any group,
 // any alignment (the reference kernel's mapping).
 template <bool BF16, bool META_HALF>
@@ -618,10 +626,13 @@ template <int SBITS, bool NIB3, bool BF16, bool META_HALF>
 int launch_kivi_rows(const KiviParams& params, int64_t body, hipStream_t stream) {
   constexpr int64_t tile_t = 8 * kivi_lane_tokens(SBITS);
   const int64_t nst = (body + tile_t - 1) / tile_t;
-  ORIGAMI_REQUIRE(params.nct * nst <= INT32_MAX, "KIVI layer exceeds the launch grid");
-  const dim3 grid(static_cast<unsigned>(params.nct * nst), 2);
+  const int64_t sink_wgs = (params.sink * (params.C / 8) + kKiviThreads - 1) / kKiviThreads;
+  ORIGAMI_REQUIRE(params.nct * nst + sink_wgs <= INT32_MAX, "KIVI layer exceeds the launch grid");
+  KiviParams p = params;
+  p.ntiles = static_cast<int32_t>(p.nct * nst);
+  const dim3 grid(static_cast<unsigned>(p.ntiles + sink_wgs), 2);
   hipLaunchKernelGGL((kivi_cache_kernel<SBITS, NIB3, BF16, META_HALF>), grid, dim3(kKiviThreads),
-                     0, stream, params);
+                     0, stream, p);
   return check_launch("kivi_cache_kernel");
 }
 
@@ -905,22 +916,6 @@ int origami_kivi_dequantize_to_kv_cache(
 #undef ORIGAMI_KIVI_GENERIC
     return check_launch("kivi_generic_kernel");
   }
-  if (sink_tokens > 0) {
-    const dim3 grid(grid_for(2 * sink_tokens * (C / 8), kDqThreads, 65536));
-    if (bf16) {
-      if (mhalf)
-        hipLaunchKernelGGL((kivi_sink_kernel<true, true>), grid, dim3(kDqThreads), 0, st, p);
-      else
-        hipLaunchKernelGGL((kivi_sink_kernel<true, false>), grid, dim3(kDqThreads), 0, st, p);
-    } else {
-      if (mhalf)
-        hipLaunchKernelGGL((kivi_sink_kernel<false, true>), grid, dim3(kDqThreads), 0, st, p);
-      else
-        hipLaunchKernelGGL((kivi_sink_kernel<false, false>), grid, dim3(kDqThreads), 0, st, p);
-    }
-    if (int rc = check_launch("kivi_sink_kernel")) return rc;
-  }
-  if (body <= 0) return ORIGAMI_OK;
   p.nct = static_cast<int32_t>((C + kKiviTileChannels - 1) / kKiviTileChannels);
   if (bf16) {
     return mhalf ? launch_kivi_cache<true, true>(p, body, sbits, nib3, st)
