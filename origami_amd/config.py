@@ -33,6 +33,8 @@ class OrigamiConfig:
     bitunpack_device: str = "auto"
     fused_attention: str = "off"
     restore_slots: int = 3
+    read_bandwidth_gbps: float = 0.0
+    artifact_ingress_mode: str = "file"
     extra: dict[str, Any] = field(default_factory=dict)
 
     @classmethod
@@ -60,6 +62,10 @@ class OrigamiConfig:
             bitunpack_device=str(get("origami_bitunpack_device", "auto")).lower(),
             fused_attention=str(get("origami_fused_attention", "off")).lower(),
             restore_slots=int(get("origami_restore_slots", 3)),
+            read_bandwidth_gbps=float(get("origami_read_bandwidth_gbps",
+                                          get("reuse_read_bandwidth_gbps", 0.0))),
+            artifact_ingress_mode=str(get("origami_artifact_ingress_mode",
+                                          get("reuse_artifact_ingress_mode", "file"))).lower(),
             extra=extra,
         )
         config.validate()
@@ -76,6 +82,14 @@ class OrigamiConfig:
             raise ValueError("Origami chunk sizes must be positive")
         if not (self.chunk_min_bytes <= self.chunk_target_bytes <= self.chunk_max_bytes):
             raise ValueError("origami_chunk_min_bytes <= target <= max is required")
+        if self.artifact_format not in {"auto", "bundle_v1", "legacy_pt"}:
+            raise ValueError("origami_artifact_format must be one of "
+                             "{'auto', 'bundle_v1', 'legacy_pt'}")
+        if self.read_bandwidth_gbps < 0:
+            raise ValueError("origami_read_bandwidth_gbps must be non-negative")
+        if self.artifact_ingress_mode not in {"file", "memory", "native-file"}:
+            raise ValueError("origami_artifact_ingress_mode must be one of "
+                             "{'file', 'memory', 'native-file'}")
         if self.bitunpack_device not in _DEVICE_POLICIES:
             raise ValueError("origami_bitunpack_device must be auto, cpu, gpu or cuda")
         if self.dequant_device not in _DEVICE_POLICIES:

@@ -170,7 +170,10 @@ class OrigamiConnectorWorker:
     def _restore_request_layer_futures(self, restore: OrigamiRestoreRequest,
                                        layer_futures: dict[str, Future]) -> str:
         try:
-            payload = self.store.prepare_for_restore(restore.cache_key)
+            payload = self.store.prepare_for_restore(
+                restore.cache_key, read_bandwidth_gbps=self.config.read_bandwidth_gbps,
+                metrics_path=self.metrics_path, request_id=restore.request_id,
+                system="origami")
             # layers are issued in model order (the kv_caches order)
             for layer_name, fut in layer_futures.items():
                 if fut.done():

@@ -55,8 +55,8 @@ def test_store_round_trip_and_missing_key():
     assert isinstance(store, InMemoryOrigamiStore)
     with pytest.raises(KeyError):
         store.get("nope")
-    with pytest.raises(ValueError):
-        create_origami_store("file:///tmp/x")
+    with pytest.raises(ValueError, match="legacy_pt"):
+        create_origami_store("file:///tmp/origami-test-x", artifact_format="legacy_pt")
 
 
 def test_adapters_byte_views():
