@@ -348,7 +348,8 @@ constexpr int kSegTokens = 16;         // tokens per lane
 constexpr int kLaneSegs = 8;           // lanes along tokens in a wave tile
 constexpr int kLaneGroups = 8;         // lanes along 16-channel groups
 constexpr int kWavePlanes = kLaneGroups * 16;  // channels per wave tile (128)
-constexpr int kMaxWq = 4;
+constexpr int kMaxWq = 16;
+constexpr int kRowsWq = 4;  // wave tiles along channels when the row is wide enough
 constexpr int kTilePlanes = kMaxWq * kWavePlanes;  // descriptor slots per workgroup
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -505,9 +506,9 @@ __device__ __forceinline__ void load_descriptors(const RowsParams& p, int64_t ti
   const int h = static_cast<int>((tile / p.nst / p.nqt) % p.H);
   const int n = p.wq * kWavePlanes;
   __syncthreads();
-  if (static_cast<int>(threadIdx.x) < n) {
-    const int64_t c = static_cast<int64_t>(qt) * n + threadIdx.x;
-    desc[threadIdx.x] = c < p.C ? p.planes[static_cast<int64_t>(h) * p.C + c] : -1;
+  for (int i = static_cast<int>(threadIdx.x); i < n; i += kRowsThreads) {
+    const int64_t c = static_cast<int64_t>(qt) * n + i;
+    desc[i] = c < p.C ? p.planes[static_cast<int64_t>(h) * p.C + c] : -1;
   }
   __syncthreads();
 }
@@ -844,7 +845,8 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
   p.C = C;
   p.nq = static_cast<int32_t>(C / 16);
   const int nqg = (p.nq + kLaneGroups - 1) / kLaneGroups;
-  p.wq = nqg >= 4 ? 4 : (nqg >= 2 ? 2 : 1);
+  p.wq = 1;
+  while (p.wq < kRowsWq && p.wq * 2 <= nqg) p.wq *= 2;
   p.ws = kRowsWaves / p.wq;
   p.nqt = (nqg + p.wq - 1) / p.wq;
   const int64_t segs = (tile_tokens_total + kSegTokens - 1) / kSegTokens;
