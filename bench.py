@@ -293,7 +293,7 @@ def dequant_leg(src_cache, T, bs, dst_cache, dst_ids, gen, dev, steps):
             read = (m["key_stream_bytes"] + m["value_stream_bytes"]
                     + 2 * sum(m[f"{k}_numel"] for k in ("key_scale", "key_zero", "value_scale",
                                                         "value_zero", "key_sink", "value_sink")))
-            kernel = "kivi_cache_kernel<2, bf16, f16 meta> + kivi_sink_kernel"
+            kernel = "kivi_cache_kernel<2, nibble=false, bf16, f16 meta> (sink rows included)"
         alg = read + out_bytes + nblk * 8
 
         def run():

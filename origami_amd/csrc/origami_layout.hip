@@ -175,6 +175,11 @@ struct PlanInfo {
   int bits = 0;              // uniform symbol width, 0 when mixed
   bool aligned16 = false;    // every plane starts on a 16-byte boundary
   bool byte_aligned = false; // every plane starts on a byte boundary
+  // Every plane p = h * C + c is covered and starts at bit dense_base + p * T *
+  // bits: the plane table is a closed form (what the chunk planner produces),
+  // so the row kernels compute descriptors instead of reading a table.
+  bool dense = false;
+  int64_t dense_base = 0;
 };
 
 // Builds the plane table: table[h*C + c] = bit offset of token 0 of plane
@@ -215,16 +220,30 @@ PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
     info.aligned16 = false;
     info.byte_aligned = false;
   }
+  if (info.regular && info.bits != 0 && H * C > 0) {
+    info.dense = true;
+    info.dense_base = table[0];
+    const int64_t stride = T * info.bits;
+    for (int64_t p = 0; p < H * C && info.dense; ++p)
+      info.dense = table[p] == info.dense_base + p * stride;
+  }
   return info;
 }
 
 struct Plan {
+  Plan() = default;
+  Plan(const Plan&) = delete;
+  Plan& operator=(const Plan&) = delete;
+  ~Plan() {
+    if (dev) (void)hipFree(dev);  // hipFree waits for work still reading it
+  }
   std::vector<int64_t> key;
   int device = -1;
   int64_t n = 0, T = 0, H = 0, C = 0, max_symbols = 0;
   PlanInfo info;
-  bool has_table = false;
-  void* dev = nullptr;  // one allocation: offsets | bits | specs | table
+  bool has_table = false;    // info was computed (row-kernel layout)
+  std::vector<int64_t> host; // offsets | bits | specs | table (table only if not dense)
+  void* dev = nullptr;       // device copy of `host`, made on first need
   const int64_t* d_offsets = nullptr;
   const int64_t* d_bits = nullptr;
   const int64_t* d_specs = nullptr;
@@ -232,8 +251,10 @@ struct Plan {
 };
 
 std::mutex g_plan_mutex;
-std::unordered_map<uint64_t, std::vector<std::unique_ptr<Plan>>> g_plans;
-size_t g_plan_count = 0;
+std::unordered_map<uint64_t, std::vector<std::shared_ptr<Plan>>> g_plans;
+size_t g_plan_count = 0;         // plans in the cache
+size_t g_plan_device_count = 0;  // of which hold device memory
+constexpr size_t kMaxHostPlans = 4096;
 
 uint64_t hash_words(const std::vector<int64_t>& w) {
   uint64_t h = 1469598103934665603ull;
@@ -246,20 +267,49 @@ uint64_t hash_words(const std::vector<int64_t>& w) {
 }
 
 void drop_all_plans() {
-  // Kernels may still read cached metadata: wait for the device first.
-  (void)hipDeviceSynchronize();
-  for (auto& kv : g_plans)
-    for (auto& p : kv.second)
-      if (p->dev) (void)hipFree(p->dev);
-  g_plans.clear();
+  // Kernels may still read cached metadata: wait for the device first (only
+  // when some plan holds device memory; dense row layouts never do).
+  if (g_plan_device_count > 0) (void)hipDeviceSynchronize();
+  g_plans.clear();  // plans a caller still holds live on until it lets go
   g_plan_count = 0;
+  g_plan_device_count = 0;
+}
+
+// Uploads the plan's metadata (chunk offsets, bits, specs and, unless the
+// layout is dense, the plane table) on first need: one hipMalloc and one
+// synchronous copy per distinct layout.
+int plan_device(const std::shared_ptr<const Plan>& cplan) {
+  Plan* plan = const_cast<Plan*>(cplan.get());
+  std::lock_guard<std::mutex> lock(g_plan_mutex);
+  if (plan->dev) return ORIGAMI_OK;
+  const size_t words = plan->host.size();
+  if (hipMalloc(&plan->dev, words * sizeof(int64_t)) != hipSuccess) {
+    plan->dev = nullptr;
+    return fail(ORIGAMI_ERR_HIP, "hipMalloc of the layout plan failed");
+  }
+  if (hipMemcpy(plan->dev, plan->host.data(), words * sizeof(int64_t), hipMemcpyHostToDevice) !=
+      hipSuccess) {
+    (void)hipFree(plan->dev);
+    plan->dev = nullptr;
+    return fail(ORIGAMI_ERR_HIP, "upload of the layout plan failed");
+  }
+  const int64_t n = plan->n;
+  const int64_t* base = static_cast<const int64_t*>(plan->dev);
+  plan->d_offsets = base;
+  plan->d_bits = base + (n + 1);
+  plan->d_specs = base + (n + 1) + n;
+  plan->d_table = words > static_cast<size_t>(8 * n + 1) ? base + (n + 1) + n + 6 * n : nullptr;
+  ++g_plan_device_count;
+  return ORIGAMI_OK;
 }
 
 // Returns the cached plan for this metadata on the current device, creating
-// it (one hipMalloc + one synchronous upload) on first use.
+// its host part on first use.  Device copies are made by plan_device(), only
+// for paths that read metadata on the device (generic kernels, row kernels
+// over a non-dense plane table).
 int get_plan(const int64_t* offsets, const int64_t* bits, const int64_t* specs,
              int64_t n, int64_t T, int64_t H, int64_t C, bool want_table,
-             const Plan** out) {
+             std::shared_ptr<const Plan>* out) {
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess)
     return fail(ORIGAMI_ERR_HIP, "hipGetDevice failed");
@@ -281,14 +331,14 @@ int get_plan(const int64_t* offsets, const int64_t* bits, const int64_t* specs,
   if (it != g_plans.end()) {
     for (auto& p : it->second) {
       if (p->key == key) {
-        *out = p.get();
+        *out = p;
         return ORIGAMI_OK;
       }
     }
   }
-  if (g_plan_count >= kMaxPlans) drop_all_plans();
+  if (g_plan_device_count >= kMaxPlans || g_plan_count >= kMaxHostPlans) drop_all_plans();
 
-  auto plan = std::make_unique<Plan>();
+  auto plan = std::make_shared<Plan>();
   plan->key = key;
   plan->device = device;
   plan->n = n;
@@ -302,30 +352,15 @@ int get_plan(const int64_t* offsets, const int64_t* bits, const int64_t* specs,
     table.resize(static_cast<size_t>(H * C));
     plan->info = build_plane_table(offsets, bits, specs, n, T, H, C, table.data());
     plan->has_table = true;
+    if (plan->info.dense) table.clear();  // the kernels compute it
   }
-  const size_t words = static_cast<size_t>((n + 1) + n + 6 * n) + table.size();
-  std::vector<int64_t> host(words);
-  size_t pos = 0;
-  std::memcpy(host.data() + pos, offsets, sizeof(int64_t) * (n + 1));
-  pos += n + 1;
-  std::memcpy(host.data() + pos, bits, sizeof(int64_t) * n);
-  pos += n;
-  std::memcpy(host.data() + pos, specs, sizeof(int64_t) * 6 * n);
-  pos += 6 * n;
-  if (!table.empty()) std::memcpy(host.data() + pos, table.data(), sizeof(int64_t) * table.size());
-  if (hipMalloc(&plan->dev, words * sizeof(int64_t)) != hipSuccess)
-    return fail(ORIGAMI_ERR_HIP, "hipMalloc of the layout plan failed");
-  if (hipMemcpy(plan->dev, host.data(), words * sizeof(int64_t), hipMemcpyHostToDevice) !=
-      hipSuccess) {
-    (void)hipFree(plan->dev);
-    return fail(ORIGAMI_ERR_HIP, "upload of the layout plan failed");
-  }
-  const int64_t* base = static_cast<const int64_t*>(plan->dev);
-  plan->d_offsets = base;
-  plan->d_bits = base + (n + 1);
-  plan->d_specs = base + (n + 1) + n;
-  plan->d_table = table.empty() ? nullptr : base + (n + 1) + n + 6 * n;
-  *out = plan.get();
+  std::vector<int64_t>& host = plan->host;
+  host.reserve(static_cast<size_t>((n + 1) + n + 6 * n) + table.size());
+  host.insert(host.end(), offsets, offsets + n + 1);
+  host.insert(host.end(), bits, bits + n);
+  host.insert(host.end(), specs, specs + 6 * n);
+  host.insert(host.end(), table.begin(), table.end());
+  *out = plan;
   g_plans[h].push_back(std::move(plan));
   ++g_plan_count;
   return ORIGAMI_OK;
@@ -358,7 +393,9 @@ struct RowsParams {
   uint8_t* stream;           // 4-byte aligned base of the flat stream
   int64_t stream_bytes;      // bytes addressable from `stream`
   int64_t bit_bias;          // (caller's stream pointer - stream) * 8
-  const int64_t* planes;     // [H*C] plane bit offsets (caller pointer based)
+  const int64_t* planes;     // [H*C] plane bit offsets (caller pointer based), or
+                             // nullptr: plane p starts at plane_base + p * plane_bits
+  int64_t plane_base, plane_bits;
   uint8_t* rows;             // row base: destination (unpack) or source (pack)
   const int64_t* block_ids;  // nullptr: identity rows
   int64_t num_blocks;        // valid block ids are [0, num_blocks)
@@ -508,7 +545,8 @@ __device__ __forceinline__ void load_descriptors(const RowsParams& p, int64_t ti
   __syncthreads();
   for (int i = static_cast<int>(threadIdx.x); i < n; i += kRowsThreads) {
     const int64_t c = static_cast<int64_t>(qt) * n + i;
-    desc[i] = c < p.C ? p.planes[static_cast<int64_t>(h) * p.C + c] : -1;
+    const int64_t plane = static_cast<int64_t>(h) * p.C + c;
+    desc[i] = c >= p.C ? -1 : p.planes ? p.planes[plane] : p.plane_base + plane * p.plane_bits;
   }
   __syncthreads();
 }
@@ -833,6 +871,20 @@ void set_stream(RowsParams& p, const uint8_t* flat, int64_t flat_bytes) {
   p.stream_bytes = flat_bytes + static_cast<int64_t>(addr - base);
 }
 
+// Points the row kernels at the plan's plane offsets: the closed form of a
+// dense plan (no device memory), or its uploaded plane table.
+int set_planes(RowsParams& p, const std::shared_ptr<const Plan>& plan) {
+  if (plan->info.dense) {
+    p.planes = nullptr;
+    p.plane_base = plan->info.dense_base;
+    p.plane_bits = plan->T * plan->info.bits;
+    return ORIGAMI_OK;
+  }
+  if (int rc = plan_device(plan)) return rc;
+  p.planes = plan->d_table;
+  return ORIGAMI_OK;
+}
+
 // Grid of the rows kernels.  When heads are contiguous inside a row
 // (head_pitch == C) and the plane table is indexed h * C + c, the heads are
 // folded into one row of H * C channels so a workgroup can span them.
@@ -965,14 +1017,14 @@ int origami_unpack_canonical_storage_chunks(
   const bool rows_layout = st.channel == 1 && C % 16 == 0 && st.token % 16 == 0 &&
                            st.head % 16 == 0 && aligned16(output) && T >= 16 &&
                            H * C <= kMaxPlaneTable;
-  const Plan* plan = nullptr;
+  std::shared_ptr<const Plan> plan;
   rc = get_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, T, H, C, rows_layout, &plan);
   if (rc) return rc;
 
   if (rows_layout && plan->has_table && plan->info.regular && plan->info.bits != 0) {
     RowsParams p{};
     set_stream(p, flat_chunks, flat_bytes);
-    p.planes = plan->d_table;
+    if (int rc2 = set_planes(p, plan)) return rc2;
     p.rows = output;
     p.block_ids = nullptr;
     p.num_blocks = 0;
@@ -989,6 +1041,8 @@ int origami_unpack_canonical_storage_chunks(
   }
 
   rc = launch_fill_zero(output, output_bytes, stream);
+  if (rc) return rc;
+  rc = plan_device(plan);
   if (rc) return rc;
   const GenericLayout L{st.token, st.head, st.channel};
   const dim3 grid(grid_for(plan->max_symbols, kThreads, 4096), static_cast<unsigned>(num_chunks));
@@ -1018,7 +1072,7 @@ int origami_pack_canonical_storage_chunks(
   const bool rows_layout = st.channel == 1 && C % 16 == 0 && st.token % 16 == 0 &&
                            st.head % 16 == 0 && aligned16(symbols) && T >= 16 &&
                            H * C <= kMaxPlaneTable;
-  const Plan* plan = nullptr;
+  std::shared_ptr<const Plan> plan;
   rc = get_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, T, H, C, rows_layout, &plan);
   if (rc) return rc;
 
@@ -1026,7 +1080,7 @@ int origami_pack_canonical_storage_chunks(
       plan->info.byte_aligned && (T * plan->info.bits) % 8 == 0) {
     RowsParams p{};
     set_stream(p, flat_chunks, flat_bytes);
-    p.planes = plan->d_table;
+    if (int rc2 = set_planes(p, plan)) return rc2;
     p.rows = const_cast<uint8_t*>(symbols);
     p.T = T;
     p.row_tokens = T;
@@ -1038,6 +1092,8 @@ int origami_pack_canonical_storage_chunks(
     return launch_rows(true, p, 1, plan->info.bits, al, stream);
   }
 
+  rc = plan_device(plan);
+  if (rc) return rc;
   const GenericLayout L{st.token, st.head, st.channel};
   int64_t max_bytes = 0;
   for (int64_t k = 0; k < num_chunks; ++k)
@@ -1071,7 +1127,7 @@ int origami_unpack_canonical_to_kv_cache(
   if (head_bytes % 16 != 0 || !aligned16(kv_cache) ||
       num_heads * head_bytes > kMaxPlaneTable)
     return fail(ORIGAMI_ERR_UNSUPPORTED, "fused restore needs 16-byte head rows");
-  const Plan* plan = nullptr;
+  std::shared_ptr<const Plan> plan;
   rc = get_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, 2 * tokens, num_heads,
                 head_bytes, true, &plan);
   if (rc) return rc;
@@ -1080,7 +1136,7 @@ int origami_unpack_canonical_to_kv_cache(
                 "fused restore needs chunks spanning all tokens with one bit width");
   RowsParams p{};
   set_stream(p, flat_chunks, flat_bytes);
-  p.planes = plan->d_table;
+  if (int rc2 = set_planes(p, plan)) return rc2;
   p.rows = static_cast<uint8_t*>(kv_cache);
   p.block_ids = block_ids;
   p.num_blocks = num_blocks;
@@ -1120,7 +1176,7 @@ int origami_pack_canonical_from_kv_cache(
   if (head_bytes % 16 != 0 || !aligned16(kv_cache) ||
       num_heads * head_bytes > kMaxPlaneTable)
     return fail(ORIGAMI_ERR_UNSUPPORTED, "fused save needs 16-byte head rows");
-  const Plan* plan = nullptr;
+  std::shared_ptr<const Plan> plan;
   rc = get_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, 2 * tokens, num_heads,
                 head_bytes, true, &plan);
   if (rc) return rc;
@@ -1130,7 +1186,7 @@ int origami_pack_canonical_from_kv_cache(
                 "fused save needs regular byte-aligned planes with one bit width");
   RowsParams p{};
   set_stream(p, flat_chunks, flat_bytes);
-  p.planes = plan->d_table;
+  if (int rc2 = set_planes(p, plan)) return rc2;
   p.rows = static_cast<uint8_t*>(const_cast<void*>(kv_cache));
   p.block_ids = block_ids;
   p.num_blocks = num_blocks;

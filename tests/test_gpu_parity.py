@@ -11,6 +11,7 @@ import torch
 
 from oracle import oracle
 from origami_amd.layout import CanonicalLayout, kv_symbol_layout
+from origami_amd import _native
 from origami_amd.lossless import native_cpu, native_gpu
 from origami_amd.lossless.chunking import plan_head_channel_chunks
 from tests import bitref
@@ -46,6 +47,8 @@ def _gpu_u8(a, dev):
 def _case_specs(kind, rng, T, H, C):
     if kind == "planner":
         return planner_specs(T, H, C, max(64, T * C // 3))
+    if kind == "reversed":  # planner boxes stored in reverse order: regular, not dense
+        return planner_specs(T, H, C, max(64, T * C // 3))[::-1].copy()
     if kind == "partition":
         return bitref.random_specs(rng, T, H, C, partition=True)
     if kind == "partial":  # a single box: the rest of the tensor is uncovered
@@ -53,7 +56,7 @@ def _case_specs(kind, rng, T, H, C):
     raise AssertionError(kind)
 
 
-@pytest.mark.parametrize("kind", ["planner", "partition", "partial"])
+@pytest.mark.parametrize("kind", ["planner", "reversed", "partition", "partial"])
 @pytest.mark.parametrize("bits", range(1, 9))
 @pytest.mark.parametrize("li", range(len(LAYOUTS)))
 def test_unpack_and_pack_match_oracle(cuda_device, li, bits, kind):
@@ -158,6 +161,40 @@ def test_save_from_kv_cache_matches_oracle(cuda_device, tokens, H, C, bs, blocks
     ids_gpu = native_gpu.block_ids_tensor(ids, cuda_device)
     flat = native_gpu.pack_from_kv_cache(cache_gpu, ids_gpu, tokens, lay)
     assert np.array_equal(flat.cpu().numpy(), ref_flat)
+
+
+@pytest.mark.parametrize("bits", [8, 5])
+def test_non_dense_plan_restore_and_save(cuda_device, bits):
+    """Planner boxes in reverse order: every plane still spans all tokens at
+    one width, so the row kernels run, reading plane offsets from the
+    uploaded plane table instead of the dense closed form."""
+    rng = np.random.default_rng(40 + bits)
+    tokens, H, C, bs = 1000, 4, 128, 16
+    specs = planner_specs(2 * tokens, H, C, 1 << 15)[::-1].copy()
+    assert len(specs) > 2
+    value = rng.integers(0, 256, (2, tokens, H, C), dtype=np.uint8)
+    flat, offs = oracle.pack_canonical(value.reshape(-1), bits, specs, [2 * tokens, H, C],
+                                       [0, 1, 2, -1])
+    ids, cache = _kv_case(rng, tokens, H, C, bs, False)
+    expect = cache.copy()
+    oracle.restore_layer(flat, offs, bits, specs, tokens, H, C, ids, expect, False)
+    cache_gpu = _gpu_u8(cache, cuda_device)
+    lay = kv_symbol_layout(tokens, H, C, bits, specs)
+    ids_gpu = native_gpu.block_ids_tensor(ids, cuda_device)
+    flat_gpu = _gpu_u8(flat, cuda_device)
+    code, nb, bsz, heads, hb = native_gpu.cache_geometry(cache_gpu)
+    stream = native_gpu._stream_handle(cuda_device)
+    # called directly: the fused entry points must accept this plan (the
+    # Python wrappers would fall back silently)
+    _native.call("origami_unpack_canonical_to_kv_cache", flat_gpu.data_ptr(), flat_gpu.numel(),
+                 *native_gpu._layout_args(lay), tokens, cache_gpu.data_ptr(), code, nb, bsz,
+                 heads, hb, ids_gpu.data_ptr(), ids_gpu.numel(), stream)
+    assert np.array_equal(cache_gpu.cpu().numpy(), expect)
+    back = torch.empty_like(flat_gpu)
+    _native.call("origami_pack_canonical_from_kv_cache", cache_gpu.data_ptr(), code, nb, bsz,
+                 heads, hb, ids_gpu.data_ptr(), ids_gpu.numel(), tokens,
+                 *native_gpu._layout_args(lay), back.data_ptr(), back.numel(), stream)
+    assert np.array_equal(back.cpu().numpy(), flat)
 
 
 def test_irregular_plan_restore_falls_back_and_matches(cuda_device):
