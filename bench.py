@@ -50,7 +50,7 @@ def parse_args():
     ap.add_argument("--bits", type=int, default=8)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-reps", type=int, default=5)
+    ap.add_argument("--cpu-reps", type=int, default=10)
     ap.add_argument("--no-pipeline", action="store_true")
     ap.add_argument("--no-dequant", action="store_true",
                     help="skip the CacheGen / KIVI fused dequantize legs")
@@ -252,7 +252,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(streams[0], layout, specs, T, H, C, bs, NB,
                                               dst_ids[0], dst_caches[0], layer_bytes,
-                                              args.cpu_reps)
+                                              args.cpu_reps, dev)
     print(json.dumps(result), flush=True)
     return 0
 
@@ -405,45 +405,148 @@ def committed_traffic(args):
     return None
 
 
-def cpu_baseline(stream, layout, specs, T, H, C, bs, NB, ids, restored_cache, layer_bytes,
-                 reps):
-    """The oracle's restore (unpack + paged scatter) of one layer on host cores."""
-    import numpy as np
-
-    from oracle import oracle
-
-    threads = min(16, os.cpu_count() or 1)
-    oracle.set_threads(threads)
-    flat = stream.cpu().numpy()
-    ids_np = ids.cpu().numpy().astype(np.int64)
-    cache = np.zeros((2, NB, bs, H, C), dtype=np.uint8)
-    times = []
-    for i in range(reps + 1):
-        t0 = time.perf_counter()
-        oracle.restore_layer(flat, layout.offsets, layout.bits, specs, T, H, C, ids_np, cache)
-        dt = time.perf_counter() - t0
-        if i:
-            times.append(dt)
-    ok = bool(np.array_equal(cache, restored_cache.view(torch_u8()).cpu().numpy()))
-    med = float(np.median(times))
+def _host_cpu_model() -> str:
     cpu_model = platform.processor() or ""
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return cpu_model
+
+
+def _time_oracle_restore(flat, layout, specs, T, H, C, ids_np, cache, threads, warmup, reps):
+    """Median seconds of the oracle's one-layer restore on `threads` host threads."""
+    import numpy as np
+
+    from oracle import oracle
+
+    oracle.set_threads(threads)
+    times = []
+    for i in range(warmup + reps):
+        t0 = time.perf_counter()
+        oracle.restore_layer(flat, layout.offsets, layout.bits, specs, T, H, C, ids_np, cache)
+        if i >= warmup:
+            times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+def _time_index_copy(value, ids, cache, threads, warmup, reps):
+    """Median seconds of torch's CPU index_copy_ of whole blocks along the
+    block dimension (the scatter of the reference's raw-bytes restore path,
+    benchmark_utils.py:434-444), on `threads` intra-op threads."""
+    import numpy as np
+    import torch
+
+    saved = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        times = []
+        for i in range(warmup + reps):
+            t0 = time.perf_counter()
+            cache.index_copy_(1, ids, value)
+            if i >= warmup:
+                times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(saved)
+    return float(np.median(times))
+
+
+def _leg(name, layer_bytes, seconds, threads, warmup, reps, sample, **extra):
+    return {"name": name, "value": round(layer_bytes / seconds / 1e9, 3), "unit": "GB/s",
+            "ms_per_layer": round(seconds * 1e3, 2), "cores": threads, "warmup": warmup,
+            "reps": reps, "sample": sample, **extra}
+
+
+def cpu_baseline(stream, layout, specs, T, H, C, bs, NB, ids, restored_cache, layer_bytes,
+                 reps, dev):
+    """Host-core baselines for the restore of one layer.
+
+    The headline (`value`) is the oracle's restore (unpack + paged scatter)
+    of one layer of the workload on all host threads (at most 16).  `legs`
+    adds the same restore on one thread, the 4096-token single-layer case
+    (block table 0..255) on all threads and on one thread, and the scatter
+    alone as the reference ships it for raw-byte payloads (torch CPU
+    index_copy_ of whole blocks, no layout transform) at the workload's
+    size.  Every oracle leg is checked against the GPU restore of the same
+    stream."""
+    import numpy as np
+    import torch
+
+    from origami_amd.layout import kv_symbol_layout
+    from origami_amd.lossless import native_gpu
+    from origami_amd.lossless.chunking import plan_head_channel_chunks
+    from origami_amd.synthetic import fill_layer
+
+    threads = min(16, os.cpu_count() or 1)
+    flat = stream.cpu().numpy()
+    ids_np = ids.cpu().numpy().astype(np.int64)
+    gpu_cache = restored_cache.view(torch_u8()).cpu().numpy()
+    cache = np.zeros((2, NB, bs, H, C), dtype=np.uint8)
+    warm = 3
+    med = _time_oracle_restore(flat, layout, specs, T, H, C, ids_np, cache, threads, warm, reps)
+    ok = bool(np.array_equal(cache, gpu_cache))
+    legs = [_leg("oracle restore, workload layer", layer_bytes, med, threads, warm, reps,
+                 f"one {T}-token layer", matches_gpu=ok)]
+    single_reps = 3
+    cache[:] = 0
+    med1 = _time_oracle_restore(flat, layout, specs, T, H, C, ids_np, cache, 1, 1, single_reps)
+    legs.append(_leg("oracle restore, workload layer", layer_bytes, med1, 1, 1, single_reps,
+                     f"one {T}-token layer", matches_gpu=bool(np.array_equal(cache, gpu_cache))))
+
+    # the scatter alone, as shipped for raw-byte payloads
+    nblk = ids_np.size
+    value = torch.from_numpy(np.resize(flat, 2 * nblk * bs * H * C)).reshape(2, nblk, bs, H, C)
+    tcache = torch.zeros((2, NB, bs, H, C), dtype=torch.uint8)
+    tids = torch.from_numpy(ids_np)
+    for th in (threads, 1):
+        sec = _time_index_copy(value, tids, tcache, th, 3, 10)
+        legs.append(_leg("raw-bytes scatter (index_copy_), workload layer", layer_bytes, sec, th,
+                         3, 10, f"one {T}-token layer of whole blocks, no layout transform"))
+    del value, tcache
+
+    # the 4096-token single-layer case: block table 0..255, seed 0
+    T1, bs1 = 4096, bs
+    nblk1 = T1 // bs1
+    plan1 = plan_head_channel_chunks(layer_index=0, num_heads=H, head_dim=C, token_count=2 * T1,
+                                     bytes_per_symbol=1, min_bytes=1 << 20, target_bytes=1 << 20,
+                                     max_bytes=1 << 20)
+    specs1 = [[c.layout.head_start, c.layout.head_end, c.layout.channel_start,
+               c.layout.channel_end, c.layout.token_start, c.layout.token_end] for c in plan1]
+    layout1 = kv_symbol_layout(T1, H, C, 8, specs1)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    ids1 = torch.arange(nblk1, dtype=torch.int64, device=dev)
+    src1 = torch.zeros((2, nblk1, bs1, H, C // 2), dtype=torch.bfloat16, device=dev)
+    fill_layer(src1, ids1, gen)
+    stream1 = native_gpu.pack_from_kv_cache(src1, ids1, T1, layout1)
+    dst1 = torch.zeros_like(src1)
+    native_gpu.unpack_to_kv_cache(stream1, layout1, T1, dst1, ids1)
+    gpu1 = dst1.view(torch_u8()).cpu().numpy()
+    flat1 = stream1.cpu().numpy()
+    bytes1 = layout1.stream_bytes + 2 * nblk1 * bs1 * H * C + nblk1 * 8
+    cache1 = np.zeros((2, nblk1, bs1, H, C), dtype=np.uint8)
+    for th in (threads, 1):
+        cache1[:] = 0
+        sec = _time_oracle_restore(flat1, layout1, specs1, T1, H, C, ids1.cpu().numpy(), cache1,
+                                   th, 3, 10)
+        legs.append(_leg("oracle restore, 4096-token layer", bytes1, sec, th, 3, 10,
+                         "one 4096-token layer, 8 heads, head_dim 128, bf16, block table 0..255",
+                         matches_gpu=bool(np.array_equal(cache1, gpu1))))
+
     return {
-        "value": round(layer_bytes / med / 1e9, 3),
+        "value": legs[0]["value"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
         "sample": (f"one layer of the workload ({T} tokens, {layer_bytes} algorithmic bytes): "
-                   f"unpack + paged scatter, OpenMP over chunks/blocks, median of {reps}"),
-        "ms_per_layer": round(med * 1e3, 2),
-        "cpu_model": cpu_model,
-        "matches_gpu": ok,
+                   f"unpack + paged scatter, OpenMP over chunks/blocks, {warm} warm-ups, "
+                   f"median of {reps}"),
+        "ms_per_layer": legs[0]["ms_per_layer"],
+        "cpu_model": _host_cpu_model(),
+        "matches_gpu": all(leg.get("matches_gpu", True) for leg in legs),
+        "legs": legs,
     }
 
 

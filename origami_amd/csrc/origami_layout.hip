@@ -175,6 +175,8 @@ struct PlanInfo {
   int bits = 0;              // uniform symbol width, 0 when mixed
   bool aligned16 = false;    // every plane starts on a 16-byte boundary
   bool byte_aligned = false; // every plane starts on a byte boundary
+  bool planes_even = false;  // every plane starts on a 2-byte boundary
+  bool planes_dword = false; // every plane starts on a 4-byte boundary
   // Every plane p = h * C + c is covered and starts at bit dense_base + p * T *
   // bits: the plane table is a closed form (what the chunk planner produces),
   // so the row kernels compute descriptors instead of reading a table.
@@ -195,6 +197,8 @@ PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
   info.bits = n > 0 ? static_cast<int>(bits[0]) : 0;
   info.aligned16 = true;
   info.byte_aligned = true;
+  info.planes_even = true;
+  info.planes_dword = true;
   for (int64_t k = 0; k < n; ++k) {
     const int64_t* s = specs + 6 * k;
     if (bits[k] != info.bits) info.bits = 0;
@@ -212,6 +216,8 @@ PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
         slot = bit_off;
         if (bit_off % 128 != 0) info.aligned16 = false;
         if (bit_off % 8 != 0) info.byte_aligned = false;
+        if (bit_off % 16 != 0) info.planes_even = false;
+        if (bit_off % 32 != 0) info.planes_dword = false;
       }
     }
   }
@@ -219,6 +225,8 @@ PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
   if (!info.regular) {
     info.aligned16 = false;
     info.byte_aligned = false;
+    info.planes_even = false;
+    info.planes_dword = false;
   }
   if (info.regular && info.bits != 0 && H * C > 0) {
     info.dense = true;
@@ -388,6 +396,18 @@ constexpr int kRowsWq = 4;  // wave tiles along channels when the row is wide en
 constexpr int kTilePlanes = kMaxWq * kWavePlanes;  // descriptor slots per workgroup
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// Multi-dword vectors at 4-byte alignment (one global load or store each).
+typedef unsigned int u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
+typedef unsigned int u32x3a4 __attribute__((ext_vector_type(3), aligned(4)));
+typedef unsigned int u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// How the row kernels address a lane's run of 16 packed symbols (2 * b bytes
+// at bit P of the stream).
+enum RowsMode : int {
+  kRowsGuarded = 0,    // any bit offset: per-dword guarded loads, byte stores
+  kRowsWindow = 1,     // runs start on even bytes (odd b) or dwords (even b)
+  kRowsAligned16 = 2,  // b = 8 and runs start on 16-byte boundaries
+};
 
 struct RowsParams {
   uint8_t* stream;           // 4-byte aligned base of the flat stream
@@ -470,11 +490,43 @@ __device__ __forceinline__ void compress16(const uint32_t (&in)[4], uint32_t* u)
   }
 }
 
+// Window-mode runs are 2b bytes, so one instruction covers less than a
+// 128-byte line per plane and the rest of each line is read or written by
+// neighbouring waves: these accesses go through the L2 normally (measured
+// up to 2x faster for the pack, and 1.2x for the restore at b = 1, than
+// non-temporal ones).
+#define ORIGAMI_RUN_LOAD(T, src) (*reinterpret_cast<const T*>(src))
+#define ORIGAMI_RUN_STORE(T, v, dst) (*reinterpret_cast<T*>(dst) = static_cast<T>(v))
+
+// Loads NU dwords from a 4-byte aligned stream address.
+template <int NU>
+__device__ __forceinline__ void load_run_dwords(const uint8_t* src, uint32_t* w) {
+  if constexpr (NU == 1) {
+    w[0] = ORIGAMI_RUN_LOAD(uint32_t, src);
+  } else if constexpr (NU == 2) {
+    const u32x2a4 x = ORIGAMI_RUN_LOAD(u32x2a4, src);
+    w[0] = x.x;
+    w[1] = x.y;
+  } else if constexpr (NU == 3) {
+    const u32x3a4 x = ORIGAMI_RUN_LOAD(u32x3a4, src);
+    w[0] = x.x;
+    w[1] = x.y;
+    w[2] = x.z;
+  } else {
+    static_assert(NU == 4, "a lane run is at most 4 dwords");
+    const u32x4a4 x = ORIGAMI_RUN_LOAD(u32x4a4, src);
+    w[0] = x.x;
+    w[1] = x.y;
+    w[2] = x.z;
+    w[3] = x.w;
+  }
+}
+
 // Loads the 16 symbols starting at stream bit P into 16 bytes.
-template <int BITS, bool ALIGNED>
+template <int BITS, int MODE>
 __device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
                                                uint32_t (&out)[4]) {
-  if constexpr (ALIGNED) {
+  if constexpr (MODE == kRowsAligned16) {
     static_assert(BITS == 8, "aligned loads are for 8-bit symbols");
     // the stream is read once: non-temporal
     const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.stream + (P >> 3)));
@@ -483,26 +535,80 @@ __device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
     out[2] = x.z;
     out[3] = x.w;
   } else {
-    constexpr int NU = (16 * BITS + 31) / 32;
-    constexpr int NW = NU + 1;
-    const int64_t d0 = P >> 5;
-    const uint32_t sh = static_cast<uint32_t>(P & 31);
-    uint32_t w[NW];
-#pragma unroll
-    for (int i = 0; i < NW; ++i) w[i] = load_dword_guarded(p.stream, (d0 + i) * 4, p.stream_bytes);
+    constexpr int NU = (16 * BITS + 31) / 32;  // = ceil(b / 2): dwords of a run
     uint32_t u[NU > 4 ? NU : 4];
+    bool loaded = false;
+    if constexpr (MODE == kRowsWindow) {
+      // The run's 2b bytes start on an even byte (on a dword when b is even),
+      // so the NU dwords from the dword at or below it hold the whole run.
+      const int64_t byte0 = (P >> 3) & ~int64_t(3);
+      if (byte0 + 4 * NU <= p.stream_bytes) {
+        uint32_t w[NU + 1];
+        load_run_dwords<NU>(p.stream + byte0, w);
+        w[NU] = 0;
+        const uint32_t sh = (BITS % 2 == 1 && ((P >> 3) & 2)) ? 16u : 0u;
 #pragma unroll
-    for (int i = 0; i < NU; ++i) u[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sh);
+        for (int i = 0; i < NU; ++i) u[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sh);
+        loaded = true;
+      }
+    }
+    if (!loaded) {
+      constexpr int NW = NU + 1;
+      const int64_t d0 = P >> 5;
+      const uint32_t sh = static_cast<uint32_t>(P & 31);
+      uint32_t w[NW];
+#pragma unroll
+      for (int i = 0; i < NW; ++i) w[i] = load_dword_guarded(p.stream, (d0 + i) * 4, p.stream_bytes);
+#pragma unroll
+      for (int i = 0; i < NU; ++i) u[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sh);
+    }
     expand16<BITS>(u, out);
   }
 }
 
 // Writes nbytes of u[] (little-endian) to dst, a byte address in the stream.
-template <bool ALIGNED>
+// kRowsWindow: nbytes is the whole run, 2b bytes at an even address (a dword
+// address when b is even), written as dwords plus at most one 2-byte store.
+template <int BITS, int MODE>
 __device__ __forceinline__ void store_stream(uint8_t* dst, const uint32_t* u, int nbytes) {
-  if constexpr (ALIGNED) {
+  constexpr int NU = (16 * BITS + 31) / 32;
+  if constexpr (MODE == kRowsAligned16) {
     const u32x4 x = {u[0], u[1], u[2], u[3]};
     __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dst));
+  } else if constexpr (MODE == kRowsWindow && BITS % 2 == 0) {
+    if constexpr (NU == 1) {
+      ORIGAMI_RUN_STORE(uint32_t, u[0], dst);
+    } else if constexpr (NU == 2) {
+      ORIGAMI_RUN_STORE(u32x2a4, (u32x2a4{u[0], u[1]}), dst);
+    } else if constexpr (NU == 3) {
+      ORIGAMI_RUN_STORE(u32x3a4, (u32x3a4{u[0], u[1], u[2]}), dst);
+    } else {
+      ORIGAMI_RUN_STORE(u32x4a4, (u32x4a4{u[0], u[1], u[2], u[3]}), dst);
+    }
+  } else if constexpr (MODE == kRowsWindow) {
+    // odd b: 2b = 4 * (NU - 1) + 2 bytes
+    uint32_t d[NU];
+    uint8_t* words = dst;
+    uint16_t* half = reinterpret_cast<uint16_t*>(dst + 4 * (NU - 1));
+    if ((reinterpret_cast<uintptr_t>(dst) & 2) == 0) {
+#pragma unroll
+      for (int i = 0; i < NU - 1; ++i) d[i] = u[i];
+      d[NU - 1] = u[NU - 1];
+    } else {  // a 2-byte head, then dwords
+      half = reinterpret_cast<uint16_t*>(dst);
+      words = dst + 2;
+#pragma unroll
+      for (int i = 0; i < NU - 1; ++i) d[i] = __builtin_amdgcn_alignbit(u[i + 1], u[i], 16);
+      d[NU - 1] = u[0];
+    }
+    if constexpr (NU - 1 == 1) {
+      ORIGAMI_RUN_STORE(uint32_t, d[0], words);
+    } else if constexpr (NU - 1 == 2) {
+      ORIGAMI_RUN_STORE(u32x2a4, (u32x2a4{d[0], d[1]}), words);
+    } else if constexpr (NU - 1 == 3) {
+      ORIGAMI_RUN_STORE(u32x3a4, (u32x3a4{d[0], d[1], d[2]}), words);
+    }
+    ORIGAMI_RUN_STORE(uint16_t, d[NU - 1], half);
   } else {
     int b = 0;
     if ((reinterpret_cast<uintptr_t>(dst) & 3) == 0) {
@@ -589,7 +695,7 @@ __device__ __forceinline__ int64_t cursor_row(const RowsParams& p, int half, con
 // Rows kernels
 // ---------------------------------------------------------------------------
 
-template <int BITS, bool ALIGNED>
+template <int BITS, int MODE>
 __device__ __forceinline__ void unpack_tile(const RowsParams& p, int64_t tile,
                                             const int64_t* desc) {
   const TileCoord tc = tile_coord(p, tile);
@@ -604,10 +710,10 @@ __device__ __forceinline__ void unpack_tile(const RowsParams& p, int64_t tile,
     if (d < 0 || nv <= 0) {
       v[k][0] = v[k][1] = v[k][2] = v[k][3] = 0;
     } else {
-      load_symbols16<BITS, ALIGNED>(p, d + p.bit_bias + sym0 * BITS, v[k]);
+      load_symbols16<BITS, MODE>(p, d + p.bit_bias + sym0 * BITS, v[k]);
     }
   }
-  if (!ALIGNED && nv < 16) {
+  if (MODE == kRowsGuarded && nv < 16) {  // other modes: T % 16 == 0
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int64_t keep = nv - 4 * m;
@@ -639,16 +745,16 @@ __device__ __forceinline__ void unpack_tile(const RowsParams& p, int64_t tile,
   }
 }
 
-template <int BITS, bool ALIGNED>
+template <int BITS, int MODE>
 __global__ __launch_bounds__(kRowsThreads) void rows_unpack_kernel(RowsParams p) {
   __shared__ int64_t desc[kTilePlanes];
   for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     load_descriptors(p, tile, desc);
-    unpack_tile<BITS, ALIGNED>(p, tile, desc);
+    unpack_tile<BITS, MODE>(p, tile, desc);
   }
 }
 
-template <int BITS, bool ALIGNED>
+template <int BITS, int MODE>
 __device__ __forceinline__ void pack_tile(const RowsParams& p, int64_t tile, const int64_t* desc) {
   const TileCoord tc = tile_coord(p, tile);
   if (tc.q >= p.nq || tc.t0 >= p.T) return;
@@ -687,16 +793,16 @@ __device__ __forceinline__ void pack_tile(const RowsParams& p, int64_t tile, con
     const int64_t P = d + p.bit_bias + sym0 * BITS;  // byte aligned by plan
     uint32_t u[NU > 4 ? NU : 4];
     compress16<BITS>(v[k], u);
-    store_stream<ALIGNED>(p.stream + (P >> 3), u, nbytes);
+    store_stream<BITS, MODE>(p.stream + (P >> 3), u, nbytes);
   }
 }
 
-template <int BITS, bool ALIGNED>
+template <int BITS, int MODE>
 __global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
   __shared__ int64_t desc[kTilePlanes];
   for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     load_descriptors(p, tile, desc);
-    pack_tile<BITS, ALIGNED>(p, tile, desc);
+    pack_tile<BITS, MODE>(p, tile, desc);
   }
 }
 
@@ -906,7 +1012,17 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
   p.nst = static_cast<int32_t>((segs + segs_per_wg - 1) / segs_per_wg);
 }
 
-int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, bool aligned,
+// Addressing mode of the row kernels for this plan and stream: `T` is the
+// symbol count per half (a multiple of 16 keeps every lane run inside its
+// plane).
+int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T) {
+  if (p.bit_bias != 0 || T % 16 != 0) return kRowsGuarded;
+  if (info.aligned16 && aligned16(p.stream)) return kRowsAligned16;
+  const bool runs_ok = info.bits % 2 == 0 ? info.planes_dword : info.planes_even;
+  return runs_ok ? kRowsWindow : kRowsGuarded;
+}
+
+int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, int mode,
                 hipStream_t stream) {
   RowsParams p = params;
   p.ntiles = nhalf * p.H * static_cast<int64_t>(p.nqt) * p.nst;
@@ -915,19 +1031,27 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, bo
   if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
   if (blocks > INT32_MAX) blocks = INT32_MAX;
   const dim3 grid(static_cast<unsigned>(blocks)), block(kRowsThreads);
-#define ORIGAMI_ROWS_CASE(B)                                                           \
-  case B:                                                                              \
-    if (pack) {                                                                        \
-      if (B == 8 && aligned)                                                           \
-        hipLaunchKernelGGL((rows_pack_kernel<8, true>), grid, block, 0, stream, p);    \
-      else                                                                             \
-        hipLaunchKernelGGL((rows_pack_kernel<B, false>), grid, block, 0, stream, p);   \
-    } else {                                                                           \
-      if (B == 8 && aligned)                                                           \
-        hipLaunchKernelGGL((rows_unpack_kernel<8, true>), grid, block, 0, stream, p);  \
-      else                                                                             \
-        hipLaunchKernelGGL((rows_unpack_kernel<B, false>), grid, block, 0, stream, p); \
-    }                                                                                  \
+  if (bits == 8 && mode == kRowsAligned16) {
+    if (pack)
+      hipLaunchKernelGGL((rows_pack_kernel<8, kRowsAligned16>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsAligned16>), grid, block, 0, stream, p);
+    return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
+  }
+  const bool window = mode == kRowsWindow;
+#define ORIGAMI_ROWS_CASE(B)                                                                  \
+  case B:                                                                                     \
+    if (pack) {                                                                               \
+      if (window)                                                                             \
+        hipLaunchKernelGGL((rows_pack_kernel<B, kRowsWindow>), grid, block, 0, stream, p);    \
+      else                                                                                    \
+        hipLaunchKernelGGL((rows_pack_kernel<B, kRowsGuarded>), grid, block, 0, stream, p);   \
+    } else {                                                                                  \
+      if (window)                                                                             \
+        hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsWindow>), grid, block, 0, stream, p);  \
+      else                                                                                    \
+        hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsGuarded>), grid, block, 0, stream, p); \
+    }                                                                                         \
     break;
   switch (bits) {
     ORIGAMI_ROWS_CASE(1)
@@ -1036,8 +1160,7 @@ int origami_unpack_canonical_storage_chunks(
     p.blk_stride = 0;
     p.half_stride = 0;
     set_grid_dims(p, H, C, T);
-    const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks);
-    return launch_rows(false, p, 1, plan->info.bits, al, stream);
+    return launch_rows(false, p, 1, plan->info.bits, rows_mode(plan->info, p, T), stream);
   }
 
   rc = launch_fill_zero(output, output_bytes, stream);
@@ -1088,8 +1211,7 @@ int origami_pack_canonical_storage_chunks(
     p.head_pitch = st.head;
     p.bs = T;
     set_grid_dims(p, H, C, T);
-    const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks) && T % 16 == 0;
-    return launch_rows(true, p, 1, plan->info.bits, al, stream);
+    return launch_rows(true, p, 1, plan->info.bits, rows_mode(plan->info, p, T), stream);
   }
 
   rc = plan_device(plan);
@@ -1148,9 +1270,7 @@ int origami_unpack_canonical_to_kv_cache(
   p.blk_stride = blk_stride;
   p.half_stride = half_stride;
   set_grid_dims(p, num_heads, head_bytes, p.row_tokens);
-  const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks) &&
-                  tokens % 16 == 0;
-  return launch_rows(false, p, 2, plan->info.bits, al, stream);
+  return launch_rows(false, p, 2, plan->info.bits, rows_mode(plan->info, p, tokens), stream);
 }
 
 int origami_pack_canonical_from_kv_cache(
@@ -1198,9 +1318,7 @@ int origami_pack_canonical_from_kv_cache(
   p.blk_stride = blk_stride;
   p.half_stride = half_stride;
   set_grid_dims(p, num_heads, head_bytes, tokens);
-  const bool al = plan->info.aligned16 && p.bit_bias == 0 && aligned16(flat_chunks) &&
-                  tokens % 16 == 0;
-  return launch_rows(true, p, 2, plan->info.bits, al, stream);
+  return launch_rows(true, p, 2, plan->info.bits, rows_mode(plan->info, p, tokens), stream);
 }
 
 static int block_copy(bool scatter, const uint8_t* src, uint8_t* dst, int64_t tokens,

@@ -143,7 +143,7 @@ def test_restore_to_kv_cache_matches_oracle(cuda_device, tokens, H, C, bs, block
 
 
 @pytest.mark.parametrize("blocks_first", [False, True])
-@pytest.mark.parametrize("bits", [8, 4, 2])
+@pytest.mark.parametrize("bits", [8, 7, 4, 3, 2, 1])
 @pytest.mark.parametrize("tokens,H,C,bs", [
     (4096, 8, 256, 16), (1000, 8, 256, 16), (2048, 8, 128, 16), (100, 2, 64, 8),
 ])
@@ -195,6 +195,34 @@ def test_non_dense_plan_restore_and_save(cuda_device, bits):
                  heads, hb, ids_gpu.data_ptr(), ids_gpu.numel(), tokens,
                  *native_gpu._layout_args(lay), back.data_ptr(), back.numel(), stream)
     assert np.array_equal(back.cpu().numpy(), flat)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 5, 6, 7])
+@pytest.mark.parametrize("shift", [0, 2, 1])
+def test_lane_runs_at_the_stream_end(cuda_device, bits, shift):
+    """Chunks covering 5 or 11 channels of one head: the stream ends 2 bytes
+    past a dword boundary for odd widths, so the last lane runs cannot use
+    the whole-dword window and take the guarded loads.  A nonzero `shift`
+    moves the stream pointer off dword alignment (guarded addressing)."""
+    rng = np.random.default_rng(bits * 10 + shift)
+    for T, specs in [(16, [[0, 1, 0, 5, 0, 16]]), (48, [[0, 1, 3, 14, 0, 48]]),
+                     (32, [[0, 1, 0, 5, 0, 32], [0, 1, 5, 16, 0, 32]])]:
+        H, C = 1, 16
+        specs = np.asarray(specs, np.int64)
+        sym = rng.integers(0, 256, T * H * C, dtype=np.uint8)
+        ref_flat, offs = oracle.pack_canonical(sym, bits, specs, [T, H, C], [0, 1, 2, -1])
+        ref_sym = oracle.unpack_canonical(ref_flat, offs, bits, specs, [T, H, C], [0, 1, 2, -1])
+        lay = CanonicalLayout.make([T, H, C], ["token", "head", "head_dim"], bits, specs)
+        buf = torch.zeros(ref_flat.size + 8, dtype=torch.uint8, device=cuda_device)
+        view = buf[shift:shift + ref_flat.size]
+        view.copy_(_gpu_u8(ref_flat, cuda_device))
+        out = native_gpu.unpack_layout(view, lay)
+        assert np.array_equal(out.cpu().numpy(), ref_sym), (T, specs.tolist())
+        buf2 = torch.full((ref_flat.size + 8,), 0xAB, dtype=torch.uint8, device=cuda_device)
+        native_gpu.pack_layout(_gpu_u8(sym, cuda_device), lay, buf2[shift:shift + ref_flat.size])
+        host = buf2.cpu().numpy()
+        assert np.array_equal(host[shift:shift + ref_flat.size], ref_flat), (T, specs.tolist())
+        assert (host[:shift] == 0xAB).all() and (host[shift + ref_flat.size:] == 0xAB).all()
 
 
 def test_irregular_plan_restore_falls_back_and_matches(cuda_device):
