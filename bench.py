@@ -233,7 +233,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": committed_traffic(args),
-            "kernel": "rows_unpack_kernel<8, true>",
+            "kernel": "rows_unpack_kernel<8, 2> (b = 8, 16-byte aligned runs)",
             "avg_launch_us": round(avg_launch_ms * 1e3, 2),
         },
         "pack_gbps": round(pack_gbps, 2),
@@ -400,7 +400,7 @@ def committed_traffic(args):
     if not default or not TRAFFIC_FILE.exists():
         return None
     for line in TRAFFIC_FILE.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch rows_unpack_kernel<8, true>:"):
+        if line.startswith("traffic_bytes_per_launch rows_unpack_kernel<8, 2>:"):
             return int(line.split(":")[1].split()[0])
     return None
 
