@@ -54,6 +54,10 @@ def parse_args():
     ap.add_argument("--no-pipeline", action="store_true")
     ap.add_argument("--no-dequant", action="store_true",
                     help="skip the CacheGen / KIVI fused dequantize legs")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the restore legs at the other KV geometries")
+    ap.add_argument("--config-layers", type=int, default=4,
+                    help="layers per geometry in the configs leg")
     ap.add_argument("--profile-only", action="store_true",
                     help="only the timed restore loop (for rocprofv3 runs)")
     ap.add_argument("--profile-dequant", action="store_true",
@@ -249,6 +253,9 @@ def main() -> int:
         result["dequant"] = dequant_leg(src_cache, T, bs, torch.zeros_like(dst_caches[0]),
                                         dst_ids[0], gen, dev, args.steps)
 
+    if not args.no_configs:
+        result["configs"] = configs_leg(dev, max(3, args.steps // 2), args.config_layers)
+
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(streams[0], layout, specs, T, H, C, bs, NB,
                                               dst_ids[0], dst_caches[0], layer_bytes,
@@ -319,6 +326,144 @@ def dequant_leg(src_cache, T, bs, dst_cache, dst_ids, gen, dev, steps):
         }
         del q, blob
     return legs
+
+
+def _planner_layout(T, H, C):
+    from origami_amd.layout import kv_symbol_layout
+    from origami_amd.lossless.chunking import plan_head_channel_chunks
+
+    plan = plan_head_channel_chunks(layer_index=0, num_heads=H, head_dim=C, token_count=2 * T,
+                                    bytes_per_symbol=1, min_bytes=1 << 20,
+                                    target_bytes=1 << 20, max_bytes=1 << 20)
+    specs = [[c.layout.head_start, c.layout.head_end, c.layout.channel_start,
+              c.layout.channel_end, c.layout.token_start, c.layout.token_end] for c in plan]
+    return kv_symbol_layout(T, H, C, 8, specs)
+
+
+def _time_restores(items, dev, steps):
+    """ms per pass over `items` = [(stream, layout, tokens, cache, ids)], with
+    events on the launch stream, after two warm-up passes."""
+    import torch
+
+    from origami_amd.lossless import native_gpu
+
+    def one_pass():
+        for stream, layout, T, cache, ids in items:
+            native_gpu.unpack_to_kv_cache(stream, layout, T, cache, ids)
+
+    for _ in range(2):
+        one_pass()
+    cur = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(cur)
+    for _ in range(steps):
+        one_pass()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _restore_round_trips(items):
+    """Every request restored into its blocks re-packs to its stream."""
+    import torch
+
+    from origami_amd.lossless import native_gpu
+
+    for stream, layout, T, cache, ids in items:
+        H, C = layout.num_heads, layout.head_dim
+        back = native_gpu.gather_kv_blocks(cache, ids).view(torch.uint8)
+        back = back.reshape(2, -1, H * C)[:, :T].contiguous().reshape(-1)
+        if not torch.equal(native_gpu.pack_layout(back, layout), stream):
+            return False
+    return True
+
+
+def configs_leg(dev, steps, layers):
+    """Restore throughput at the other KV geometries, `layers` layers each
+    (every layer has its own paged cache and streams; a pass restores every
+    request of every layer, one fused launch per request and layer):
+
+    * qwen2.5-7b-batch: 4 KV heads, head_dim 128, bf16, bs 16; 8 requests of
+      U[8192, 65536] tokens (seed 2) whose first floor(T/2/bs) blocks come
+      from a prefix pool shared by all block tables (the same destination
+      blocks are written by several requests); bytes are reported counting
+      each destination block once (`gbps`) and per write (`gbps_with_repeats`);
+    * llama3-8b-fp8-16x16k: 8 KV heads, head_dim 128, float8_e4m3fn (128-byte
+      head rows), 16 requests of 16384 tokens;
+    * llama3-70b-128k: 8 KV heads, head_dim 128, bf16, one 131072-token
+      request per layer.
+
+    All use 1 MiB planner chunks, bits 8, and permuted block tables."""
+    import numpy as np
+    import torch
+
+    from origami_amd.lossless import native_gpu
+    from origami_amd.synthetic import fill_layer
+
+    bs = 16
+    out = {}
+
+    def build(name, H, D, dtype, lengths, seed, shared_pool):
+        esize = torch.empty((), dtype=dtype).element_size()
+        C = D * esize
+        rng = np.random.default_rng(seed)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        nblks = [-(-int(T) // bs) for T in lengths]
+        pool = max(int(T) // 2 // bs for T in lengths) if shared_pool else 0
+        shared = [int(T) // 2 // bs if shared_pool else 0 for T in lengths]
+        NB = pool + sum(n - k for n, k in zip(nblks, shared)) + 64
+        layouts = {int(T): _planner_layout(int(T), H, C) for T in set(lengths)}
+        src = torch.zeros((2, NB, bs, H, D), dtype=dtype, device=dev)
+        items, alg_unique, alg_repeats = [], 0, 0
+        for _ in range(layers):
+            fill_layer(src, torch.arange(NB, device=dev), gen)
+
+            def tables():
+                perm = rng.permutation(NB)
+                cur, ts = pool, []
+                for n, k in zip(nblks, shared):
+                    ts.append(np.concatenate([perm[:k], perm[cur:cur + n - k]]).astype(np.int64))
+                    cur += n - k
+                return ts
+
+            cache = torch.zeros((2, NB, bs, H, D), dtype=dtype, device=dev)
+            for T, st, dt in zip(lengths, tables(), tables()):
+                lay = layouts[int(T)]
+                stream = native_gpu.pack_from_kv_cache(src, native_gpu.block_ids_tensor(st, dev, NB),
+                                                       int(T), lay)
+                items.append((stream, lay, int(T), cache, native_gpu.block_ids_tensor(dt, dev, NB)))
+                alg_repeats += lay.stream_bytes + 2 * dt.size * bs * H * C + 8 * dt.size
+            written = len(np.unique(np.concatenate([it[4].cpu().numpy() for it in items
+                                                    if it[3] is cache])))
+            alg_unique += (sum(it[1].stream_bytes + 8 * it[4].numel() for it in items
+                               if it[3] is cache) + 2 * written * bs * H * C)
+        del src
+        ms = _time_restores(items, dev, steps)
+        ok = _restore_round_trips(items[-len(lengths):])
+        res = {
+            "layers": layers, "requests_per_layer": len(lengths),
+            "tokens_per_layer": int(sum(int(T) for T in lengths)),
+            "kv_heads": H, "head_dim": D, "kv_dtype": str(dtype).replace("torch.", ""),
+            "per_layer_us": round(1e3 * ms / layers, 2),
+            "algorithmic_bytes_per_layer": int(alg_unique // layers),
+            "gbps": round(alg_unique / (ms * 1e-3) / 1e9, 2),
+            "frac": round(alg_unique / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "restore_ok": ok,
+        }
+        if shared_pool:
+            res["gbps_with_repeats"] = round(alg_repeats / (ms * 1e-3) / 1e9, 2)
+            res["algorithmic_bytes_per_layer_with_repeats"] = int(alg_repeats // layers)
+        out[name] = res
+        del items
+        torch.cuda.empty_cache()
+
+    lengths = np.random.default_rng(2).integers(8192, 65537, 8)
+    build("qwen2.5-7b-batch", 4, 128, torch.bfloat16, lengths, 2, True)
+    build("llama3-8b-fp8-16x16k", 8, 128, torch.float8_e4m3fn, [16384] * 16, 3, False)
+    build("llama3-70b-128k", 8, 128, torch.bfloat16, [131072], 4, False)
+    return out
 
 
 def pipeline_leg(streams, layout, T, dst_caches, dst_ids, dev, kernel_ms):

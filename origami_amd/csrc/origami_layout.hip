@@ -27,6 +27,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <atomic>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -382,11 +383,14 @@ constexpr int kThreads = 256;          // generic and block-copy kernels
 
 // Rows kernels: a lane owns 16 channels x 16 tokens; a wave tile is 8 lanes
 // along channels x 8 lanes along tokens (128 channels x 128 tokens); a
-// workgroup is 16 wave tiles arranged wq x (16 / wq), wq <= 4, i.e. up to
-// 512 channels x 512 tokens.  Large tiles keep both the plane runs read and the
-// row segments written long (512 B at wq = 4), which is what HBM rewards.
-constexpr int kRowsWaves = 16;
-constexpr int kRowsThreads = kRowsWaves * 64;
+// workgroup is normally 16 wave tiles arranged wq x (16 / wq), wq <= 4, i.e.
+// up to 512 channels x 512 tokens.  Large tiles keep both the plane runs read
+// and the row segments written long (512 B at wq = 4), which is what HBM
+// rewards.  A launch with too few such tiles to give every CU two uses 8- or
+// 4-wave workgroups (wq <= 2) instead: a CU only moves about 1/256 of HBM
+// bandwidth, so idle CUs cost more than short runs.
+constexpr int kRowsMaxWaves = 16;
+constexpr int kRowsThreads = kRowsMaxWaves * 64;  // launch bound
 constexpr int kSegTokens = 16;         // tokens per lane
 constexpr int kLaneSegs = 8;           // lanes along tokens in a wave tile
 constexpr int kLaneGroups = 8;         // lanes along 16-channel groups
@@ -407,6 +411,7 @@ enum RowsMode : int {
   kRowsGuarded = 0,    // any bit offset: per-dword guarded loads, byte stores
   kRowsWindow = 1,     // runs start on even bytes (odd b) or dwords (even b)
   kRowsAligned16 = 2,  // b = 8 and runs start on 16-byte boundaries
+  kRowsBytes = 3,      // unpack only: runs start on byte boundaries, any token count
 };
 
 struct RowsParams {
@@ -429,8 +434,9 @@ struct RowsParams {
   int64_t half_stride;       // rows per half step
   int32_t H;
   int32_t nq;                // C / 16
+  int32_t waves;             // waves per workgroup (16, 8 or 4)
   int32_t wq;                // wave tiles along channels per workgroup (1, 2, 4)
-  int32_t ws;                // wave tiles along tokens per workgroup (16 / wq)
+  int32_t ws;                // wave tiles along tokens per workgroup (waves / wq)
   int32_t nqt;               // workgroups along channels
   int32_t nst;               // workgroups along tokens
   int64_t ntiles;            // workgroup tiles; a workgroup loops over tiles
@@ -552,6 +558,26 @@ __device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
         loaded = true;
       }
     }
+    if constexpr (MODE == kRowsBytes) {
+      // The run's 2b bytes start on a byte: the NB dwords from the dword at or
+      // below it hold it whatever the byte's position in its dword.
+      constexpr int NB = (3 + 2 * BITS + 3) / 4;
+      const int64_t byte = P >> 3;
+      const int64_t byte0 = byte & ~int64_t(3);
+      if (byte0 + 4 * NB <= p.stream_bytes) {
+        uint32_t w[5];
+        if constexpr (NB == 5) {
+          load_run_dwords<4>(p.stream + byte0, w);
+          load_run_dwords<1>(p.stream + byte0 + 16, w + 4);
+        } else {
+          load_run_dwords<NB>(p.stream + byte0, w);
+        }
+        const uint32_t sh = static_cast<uint32_t>(byte & 3) * 8u;
+#pragma unroll
+        for (int i = 0; i < NU; ++i) u[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sh);
+        loaded = true;
+      }
+    }
     if (!loaded) {
       constexpr int NW = NU + 1;
       const int64_t d0 = P >> 5;
@@ -649,7 +675,7 @@ __device__ __forceinline__ void load_descriptors(const RowsParams& p, int64_t ti
   const int h = static_cast<int>((tile / p.nst / p.nqt) % p.H);
   const int n = p.wq * kWavePlanes;
   __syncthreads();
-  for (int i = static_cast<int>(threadIdx.x); i < n; i += kRowsThreads) {
+  for (int i = static_cast<int>(threadIdx.x); i < n; i += static_cast<int>(blockDim.x)) {
     const int64_t c = static_cast<int64_t>(qt) * n + i;
     const int64_t plane = static_cast<int64_t>(h) * p.C + c;
     desc[i] = c >= p.C ? -1 : p.planes ? p.planes[plane] : p.plane_base + plane * p.plane_bits;
@@ -713,7 +739,7 @@ __device__ __forceinline__ void unpack_tile(const RowsParams& p, int64_t tile,
       load_symbols16<BITS, MODE>(p, d + p.bit_bias + sym0 * BITS, v[k]);
     }
   }
-  if (MODE == kRowsGuarded && nv < 16) {  // other modes: T % 16 == 0
+  if ((MODE == kRowsGuarded || MODE == kRowsBytes) && nv < 16) {  // others: T % 16 == 0
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int64_t keep = nv - 4 * m;
@@ -991,10 +1017,28 @@ int set_planes(RowsParams& p, const std::shared_ptr<const Plan>& plan) {
   return ORIGAMI_OK;
 }
 
+// Compute units of the current device (cached per device).
+int device_cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 // Grid of the rows kernels.  When heads are contiguous inside a row
 // (head_pitch == C) and the plane table is indexed h * C + c, the heads are
-// folded into one row of H * C channels so a workgroup can span them.
-void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_total) {
+// folded into one row of H * C channels so a workgroup can span them.  The
+// workgroup is the largest of 16, 8 or 4 waves that still gives at least two
+// workgroups per CU over `nhalf` halves of `tile_tokens_total` tokens.
+void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_total,
+                   int64_t nhalf) {
   if (H > 1 && p.head_pitch == C) {
     C *= H;
     H = 1;
@@ -1003,23 +1047,36 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
   p.C = C;
   p.nq = static_cast<int32_t>(C / 16);
   const int nqg = (p.nq + kLaneGroups - 1) / kLaneGroups;
-  p.wq = 1;
-  while (p.wq < kRowsWq && p.wq * 2 <= nqg) p.wq *= 2;
-  p.ws = kRowsWaves / p.wq;
-  p.nqt = (nqg + p.wq - 1) / p.wq;
   const int64_t segs = (tile_tokens_total + kSegTokens - 1) / kSegTokens;
-  const int64_t segs_per_wg = static_cast<int64_t>(p.ws) * kLaneSegs;
-  p.nst = static_cast<int32_t>((segs + segs_per_wg - 1) / segs_per_wg);
+  const int64_t want = 2 * static_cast<int64_t>(device_cu_count());
+  for (int waves = kRowsMaxWaves;; waves /= 2) {
+    const int wq_cap = waves == kRowsMaxWaves ? kRowsWq : 2;
+    int wq = 1;
+    while (wq < wq_cap && wq * 2 <= nqg) wq *= 2;
+    p.waves = waves;
+    p.wq = wq;
+    p.ws = waves / wq;
+    p.nqt = (nqg + wq - 1) / wq;
+    const int64_t segs_per_wg = static_cast<int64_t>(p.ws) * kLaneSegs;
+    p.nst = static_cast<int32_t>((segs + segs_per_wg - 1) / segs_per_wg);
+    const int64_t tiles = nhalf * H * static_cast<int64_t>(p.nqt) * p.nst;
+    if (tiles >= want || waves == 4) break;
+  }
 }
 
 // Addressing mode of the row kernels for this plan and stream: `T` is the
 // symbol count per half (a multiple of 16 keeps every lane run inside its
 // plane).
-int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T) {
-  if (p.bit_bias != 0 || T % 16 != 0) return kRowsGuarded;
-  if (info.aligned16 && aligned16(p.stream)) return kRowsAligned16;
-  const bool runs_ok = info.bits % 2 == 0 ? info.planes_dword : info.planes_even;
-  return runs_ok ? kRowsWindow : kRowsGuarded;
+int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack) {
+  if (p.bit_bias == 0 && T % 16 == 0) {
+    if (info.aligned16 && aligned16(p.stream)) return kRowsAligned16;
+    const bool runs_ok = info.bits % 2 == 0 ? info.planes_dword : info.planes_even;
+    if (runs_ok) return kRowsWindow;
+  }
+  // bit_bias is a whole number of bytes, so runs start on bytes when every
+  // plane does and a half's symbols fill whole bytes
+  if (!pack && info.byte_aligned && (T * info.bits) % 8 == 0) return kRowsBytes;
+  return kRowsGuarded;
 }
 
 int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, int mode,
@@ -1030,7 +1087,7 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
   int64_t blocks = p.ntiles;
   if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
   if (blocks > INT32_MAX) blocks = INT32_MAX;
-  const dim3 grid(static_cast<unsigned>(blocks)), block(kRowsThreads);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(64 * p.waves));
   if (bits == 8 && mode == kRowsAligned16) {
     if (pack)
       hipLaunchKernelGGL((rows_pack_kernel<8, kRowsAligned16>), grid, block, 0, stream, p);
@@ -1039,6 +1096,7 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
     return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
   }
   const bool window = mode == kRowsWindow;
+  const bool bytes = mode == kRowsBytes && !pack;
 #define ORIGAMI_ROWS_CASE(B)                                                                  \
   case B:                                                                                     \
     if (pack) {                                                                               \
@@ -1049,6 +1107,8 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
     } else {                                                                                  \
       if (window)                                                                             \
         hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsWindow>), grid, block, 0, stream, p);  \
+      else if (bytes)                                                                         \
+        hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsBytes>), grid, block, 0, stream, p);   \
       else                                                                                    \
         hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsGuarded>), grid, block, 0, stream, p); \
     }                                                                                         \
@@ -1159,8 +1219,9 @@ int origami_unpack_canonical_storage_chunks(
     p.bs = T;
     p.blk_stride = 0;
     p.half_stride = 0;
-    set_grid_dims(p, H, C, T);
-    return launch_rows(false, p, 1, plan->info.bits, rows_mode(plan->info, p, T), stream);
+    set_grid_dims(p, H, C, T, 1);
+    return launch_rows(false, p, 1, plan->info.bits, rows_mode(plan->info, p, T, false),
+                       stream);
   }
 
   rc = launch_fill_zero(output, output_bytes, stream);
@@ -1210,8 +1271,8 @@ int origami_pack_canonical_storage_chunks(
     p.row_pitch = st.token;
     p.head_pitch = st.head;
     p.bs = T;
-    set_grid_dims(p, H, C, T);
-    return launch_rows(true, p, 1, plan->info.bits, rows_mode(plan->info, p, T), stream);
+    set_grid_dims(p, H, C, T, 1);
+    return launch_rows(true, p, 1, plan->info.bits, rows_mode(plan->info, p, T, true), stream);
   }
 
   rc = plan_device(plan);
@@ -1269,8 +1330,9 @@ int origami_unpack_canonical_to_kv_cache(
   p.bs = block_size;
   p.blk_stride = blk_stride;
   p.half_stride = half_stride;
-  set_grid_dims(p, num_heads, head_bytes, p.row_tokens);
-  return launch_rows(false, p, 2, plan->info.bits, rows_mode(plan->info, p, tokens), stream);
+  set_grid_dims(p, num_heads, head_bytes, p.row_tokens, 2);
+  return launch_rows(false, p, 2, plan->info.bits, rows_mode(plan->info, p, tokens, false),
+                     stream);
 }
 
 int origami_pack_canonical_from_kv_cache(
@@ -1317,8 +1379,9 @@ int origami_pack_canonical_from_kv_cache(
   p.bs = block_size;
   p.blk_stride = blk_stride;
   p.half_stride = half_stride;
-  set_grid_dims(p, num_heads, head_bytes, tokens);
-  return launch_rows(true, p, 2, plan->info.bits, rows_mode(plan->info, p, tokens), stream);
+  set_grid_dims(p, num_heads, head_bytes, tokens, 2);
+  return launch_rows(true, p, 2, plan->info.bits, rows_mode(plan->info, p, tokens, true),
+                     stream);
 }
 
 static int block_copy(bool scatter, const uint8_t* src, uint8_t* dst, int64_t tokens,

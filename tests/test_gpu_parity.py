@@ -163,6 +163,31 @@ def test_save_from_kv_cache_matches_oracle(cuda_device, tokens, H, C, bs, blocks
     assert np.array_equal(flat.cpu().numpy(), ref_flat)
 
 
+@pytest.mark.parametrize("blocks_first", [False, True])
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("tokens", [16384, 8192])
+def test_smaller_workgroups_restore_and_save(cuda_device, tokens, bits, blocks_first):
+    """Launches with fewer than two 16-wave tiles per CU run 8- or 4-wave
+    workgroups (2048-byte rows: 16384 tokens -> 8 waves, 8192 -> 4 waves on
+    a 256-CU device)."""
+    rng = np.random.default_rng(tokens + bits)
+    H, C, bs = 8, 256, 16
+    specs = planner_specs(2 * tokens, H, C, 1 << 20)
+    value = rng.integers(0, 256, (2, tokens, H, C), dtype=np.uint8)
+    flat, offs = oracle.pack_canonical(value.reshape(-1), bits, specs, [2 * tokens, H, C],
+                                       [0, 1, 2, -1])
+    ids, cache = _kv_case(rng, tokens, H, C, bs, blocks_first)
+    expect = cache.copy()
+    oracle.restore_layer(flat, offs, bits, specs, tokens, H, C, ids, expect, blocks_first)
+    cache_gpu = _gpu_u8(cache, cuda_device)
+    lay = kv_symbol_layout(tokens, H, C, bits, specs)
+    ids_gpu = native_gpu.block_ids_tensor(ids, cuda_device)
+    native_gpu.unpack_to_kv_cache(_gpu_u8(flat, cuda_device), lay, tokens, cache_gpu, ids_gpu)
+    assert np.array_equal(cache_gpu.cpu().numpy(), expect)
+    back = native_gpu.pack_from_kv_cache(cache_gpu, ids_gpu, tokens, lay)
+    assert np.array_equal(back.cpu().numpy(), flat)
+
+
 @pytest.mark.parametrize("bits", [8, 5])
 def test_non_dense_plan_restore_and_save(cuda_device, bits):
     """Planner boxes in reverse order: every plane still spans all tokens at
