@@ -408,10 +408,10 @@ typedef unsigned int u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 // How the row kernels address a lane's run of 16 packed symbols (2 * b bytes
 // at bit P of the stream).
 enum RowsMode : int {
-  kRowsGuarded = 0,    // any bit offset: per-dword guarded loads, byte stores
   kRowsWindow = 1,     // runs start on even bytes (odd b) or dwords (even b)
   kRowsAligned16 = 2,  // b = 8 and runs start on 16-byte boundaries
-  kRowsBytes = 3,      // unpack only: runs start on byte boundaries, any token count
+  kRowsShift = 3,      // unpack: runs start at any bit, any token count
+  kRowsBytes = 4,      // pack: runs start on bytes, any token count
 };
 
 struct RowsParams {
@@ -558,12 +558,11 @@ __device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
         loaded = true;
       }
     }
-    if constexpr (MODE == kRowsBytes) {
-      // The run's 2b bytes start on a byte: the NB dwords from the dword at or
-      // below it hold it whatever the byte's position in its dword.
-      constexpr int NB = (3 + 2 * BITS + 3) / 4;
-      const int64_t byte = P >> 3;
-      const int64_t byte0 = byte & ~int64_t(3);
+    if constexpr (MODE == kRowsShift) {
+      // The run's 16b bits start at any bit: the NU + 1 dwords from the one
+      // holding its first bit hold it.
+      constexpr int NB = NU + 1;
+      const int64_t byte0 = (P >> 5) * 4;
       if (byte0 + 4 * NB <= p.stream_bytes) {
         uint32_t w[5];
         if constexpr (NB == 5) {
@@ -572,13 +571,13 @@ __device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
         } else {
           load_run_dwords<NB>(p.stream + byte0, w);
         }
-        const uint32_t sh = static_cast<uint32_t>(byte & 3) * 8u;
+        const uint32_t sh = static_cast<uint32_t>(P & 31);
 #pragma unroll
         for (int i = 0; i < NU; ++i) u[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sh);
         loaded = true;
       }
     }
-    if (!loaded) {
+    if (!loaded) {  // the window would pass the end of the stream
       constexpr int NW = NU + 1;
       const int64_t d0 = P >> 5;
       const uint32_t sh = static_cast<uint32_t>(P & 31);
@@ -595,6 +594,7 @@ __device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
 // Writes nbytes of u[] (little-endian) to dst, a byte address in the stream.
 // kRowsWindow: nbytes is the whole run, 2b bytes at an even address (a dword
 // address when b is even), written as dwords plus at most one 2-byte store.
+// kRowsBytes: any byte address and any nbytes <= 2b.
 template <int BITS, int MODE>
 __device__ __forceinline__ void store_stream(uint8_t* dst, const uint32_t* u, int nbytes) {
   constexpr int NU = (16 * BITS + 31) / 32;
@@ -636,11 +636,42 @@ __device__ __forceinline__ void store_stream(uint8_t* dst, const uint32_t* u, in
     }
     ORIGAMI_RUN_STORE(uint16_t, d[NU - 1], half);
   } else {
-    int b = 0;
-    if ((reinterpret_cast<uintptr_t>(dst) & 3) == 0) {
-      for (; b + 4 <= nbytes; b += 4) *reinterpret_cast<uint32_t*>(dst + b) = u[b >> 2];
+    static_assert(MODE == kRowsBytes, "pack modes: aligned16, window, bytes");
+    // nbytes <= 2b bytes at any byte address: up to 3 head bytes to the next
+    // dword, whole dwords, then up to 3 tail bytes.  Byte j of the run is
+    // byte j & 3 of u[j >> 2].
+    uint32_t w[NU + 1];
+#pragma unroll
+    for (int i = 0; i < NU; ++i) w[i] = u[i];
+    w[NU] = 0;
+    const int head =
+        min(static_cast<int>((4u - (reinterpret_cast<uintptr_t>(dst) & 3u)) & 3u), nbytes);
+    if (head == 0 && nbytes == 4 * NU) {  // a whole run of even b at a dword address
+      if constexpr (NU == 1) {
+        ORIGAMI_RUN_STORE(uint32_t, u[0], dst);
+      } else if constexpr (NU == 2) {
+        ORIGAMI_RUN_STORE(u32x2a4, (u32x2a4{u[0], u[1]}), dst);
+      } else if constexpr (NU == 3) {
+        ORIGAMI_RUN_STORE(u32x3a4, (u32x3a4{u[0], u[1], u[2]}), dst);
+      } else {
+        ORIGAMI_RUN_STORE(u32x4a4, (u32x4a4{u[0], u[1], u[2], u[3]}), dst);
+      }
+      return;
     }
-    for (; b < nbytes; ++b) dst[b] = static_cast<uint8_t>(u[b >> 2] >> (8 * (b & 3)));
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      if (j < head) dst[j] = static_cast<uint8_t>(w[0] >> (8 * j));
+    const uint32_t sh = 8u * static_cast<uint32_t>(head);
+    const int ndw = (nbytes - head) >> 2;
+#pragma unroll
+    for (int k = 0; k < NU; ++k)
+      if (k < ndw)
+        *reinterpret_cast<uint32_t*>(dst + head + 4 * k) =
+            __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
+    const int tail0 = head + 4 * ndw;
+#pragma unroll
+    for (int j = 0; j < 2 * BITS; ++j)
+      if (j >= tail0 && j < nbytes) dst[j] = static_cast<uint8_t>(w[j >> 2] >> (8 * (j & 3)));
   }
 }
 
@@ -739,7 +770,7 @@ __device__ __forceinline__ void unpack_tile(const RowsParams& p, int64_t tile,
       load_symbols16<BITS, MODE>(p, d + p.bit_bias + sym0 * BITS, v[k]);
     }
   }
-  if ((MODE == kRowsGuarded || MODE == kRowsBytes) && nv < 16) {  // others: T % 16 == 0
+  if (MODE == kRowsShift && nv < 16) {  // other modes: T % 16 == 0
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int64_t keep = nv - 4 * m;
@@ -1066,17 +1097,15 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
 
 // Addressing mode of the row kernels for this plan and stream: `T` is the
 // symbol count per half (a multiple of 16 keeps every lane run inside its
-// plane).
+// plane).  The rows pack is only launched for byte-aligned planes with T * b
+// a multiple of 8, so its runs always start on bytes.
 int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack) {
   if (p.bit_bias == 0 && T % 16 == 0) {
     if (info.aligned16 && aligned16(p.stream)) return kRowsAligned16;
     const bool runs_ok = info.bits % 2 == 0 ? info.planes_dword : info.planes_even;
     if (runs_ok) return kRowsWindow;
   }
-  // bit_bias is a whole number of bytes, so runs start on bytes when every
-  // plane does and a half's symbols fill whole bytes
-  if (!pack && info.byte_aligned && (T * info.bits) % 8 == 0) return kRowsBytes;
-  return kRowsGuarded;
+  return pack ? kRowsBytes : kRowsShift;
 }
 
 int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, int mode,
@@ -1096,21 +1125,18 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
     return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
   }
   const bool window = mode == kRowsWindow;
-  const bool bytes = mode == kRowsBytes && !pack;
 #define ORIGAMI_ROWS_CASE(B)                                                                  \
   case B:                                                                                     \
     if (pack) {                                                                               \
       if (window)                                                                             \
         hipLaunchKernelGGL((rows_pack_kernel<B, kRowsWindow>), grid, block, 0, stream, p);    \
       else                                                                                    \
-        hipLaunchKernelGGL((rows_pack_kernel<B, kRowsGuarded>), grid, block, 0, stream, p);   \
+        hipLaunchKernelGGL((rows_pack_kernel<B, kRowsBytes>), grid, block, 0, stream, p);     \
     } else {                                                                                  \
       if (window)                                                                             \
         hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsWindow>), grid, block, 0, stream, p);  \
-      else if (bytes)                                                                         \
-        hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsBytes>), grid, block, 0, stream, p);   \
       else                                                                                    \
-        hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsGuarded>), grid, block, 0, stream, p); \
+        hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsShift>), grid, block, 0, stream, p);   \
     }                                                                                         \
     break;
   switch (bits) {
