@@ -392,9 +392,12 @@ def configs_leg(dev, steps, layers):
     * llama3-8b-fp8-16x16k: 8 KV heads, head_dim 128, float8_e4m3fn (128-byte
       head rows), 16 requests of 16384 tokens;
     * llama3-70b-128k: 8 KV heads, head_dim 128, bf16, one 131072-token
-      request per layer.
+      request per layer;
+    * llama3-8b-4k: one layer of one 4096-token request, 8 KV heads,
+      head_dim 128, bf16, block table 0..255 (a launch-bound size).
 
-    All use 1 MiB planner chunks, bits 8, and permuted block tables."""
+    All use 1 MiB planner chunks and bits 8; the tables are permuted except
+    for the 4096-token case."""
     import numpy as np
     import torch
 
@@ -404,7 +407,7 @@ def configs_leg(dev, steps, layers):
     bs = 16
     out = {}
 
-    def build(name, H, D, dtype, lengths, seed, shared_pool):
+    def build(name, H, D, dtype, lengths, seed, shared_pool, identity=False, nlayers=layers):
         esize = torch.empty((), dtype=dtype).element_size()
         C = D * esize
         rng = np.random.default_rng(seed)
@@ -417,11 +420,11 @@ def configs_leg(dev, steps, layers):
         layouts = {int(T): _planner_layout(int(T), H, C) for T in set(lengths)}
         src = torch.zeros((2, NB, bs, H, D), dtype=dtype, device=dev)
         items, alg_unique, alg_repeats = [], 0, 0
-        for _ in range(layers):
+        for _ in range(nlayers):
             fill_layer(src, torch.arange(NB, device=dev), gen)
 
             def tables():
-                perm = rng.permutation(NB)
+                perm = np.arange(NB) if identity else rng.permutation(NB)
                 cur, ts = pool, []
                 for n, k in zip(nblks, shared):
                     ts.append(np.concatenate([perm[:k], perm[cur:cur + n - k]]).astype(np.int64))
@@ -443,22 +446,23 @@ def configs_leg(dev, steps, layers):
         ms = _time_restores(items, dev, steps)
         ok = _restore_round_trips(items[-len(lengths):])
         res = {
-            "layers": layers, "requests_per_layer": len(lengths),
+            "layers": nlayers, "requests_per_layer": len(lengths),
             "tokens_per_layer": int(sum(int(T) for T in lengths)),
             "kv_heads": H, "head_dim": D, "kv_dtype": str(dtype).replace("torch.", ""),
-            "per_layer_us": round(1e3 * ms / layers, 2),
-            "algorithmic_bytes_per_layer": int(alg_unique // layers),
+            "per_layer_us": round(1e3 * ms / nlayers, 2),
+            "algorithmic_bytes_per_layer": int(alg_unique // nlayers),
             "gbps": round(alg_unique / (ms * 1e-3) / 1e9, 2),
             "frac": round(alg_unique / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
             "restore_ok": ok,
         }
         if shared_pool:
             res["gbps_with_repeats"] = round(alg_repeats / (ms * 1e-3) / 1e9, 2)
-            res["algorithmic_bytes_per_layer_with_repeats"] = int(alg_repeats // layers)
+            res["algorithmic_bytes_per_layer_with_repeats"] = int(alg_repeats // nlayers)
         out[name] = res
         del items
         torch.cuda.empty_cache()
 
+    build("llama3-8b-4k", 8, 128, torch.bfloat16, [4096], 0, False, identity=True, nlayers=1)
     lengths = np.random.default_rng(2).integers(8192, 65537, 8)
     build("qwen2.5-7b-batch", 4, 128, torch.bfloat16, lengths, 2, True)
     build("llama3-8b-fp8-16x16k", 8, 128, torch.float8_e4m3fn, [16384] * 16, 3, False)
@@ -679,6 +683,25 @@ def cpu_baseline(stream, layout, specs, T, H, C, bs, NB, ids, restored_cache, la
         legs.append(_leg("oracle restore, 4096-token layer", bytes1, sec, th, 3, 10,
                          "one 4096-token layer, 8 heads, head_dim 128, bf16, block table 0..255",
                          matches_gpu=bool(np.array_equal(cache1, gpu1))))
+
+    # context: the CPU codec (zlib level 1, raw deflate) over the 4096-token
+    # layer's chunks, one thread
+    from origami_amd.lossless.cpu_qat import CpuLosslessCodec
+
+    codec = CpuLosslessCodec(backend="zlib")
+    chunks = [stream1[int(a):int(b)].cpu() for a, b in zip(layout1.offsets[:-1],
+                                                           layout1.offsets[1:])]
+    t0 = time.perf_counter()
+    comp = codec.compress_many(chunks)
+    t_comp = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    back = codec.decompress_many(comp, [c.numel() for c in chunks])
+    t_dec = time.perf_counter() - t0
+    zok = all(bool(torch.equal(a, b)) for a, b in zip(back, chunks))
+    legs.append({"name": "zlib level 1 (context), 4096-token layer stream",
+                 "compress_ms": round(t_comp * 1e3, 2), "decompress_ms": round(t_dec * 1e3, 2),
+                 "ratio": round(layout1.stream_bytes / sum(c.numel() for c in comp), 3),
+                 "round_trip_ok": zok, "sample": f"{len(chunks)} chunks of 1 MiB"})
 
     return {
         "value": legs[0]["value"],
