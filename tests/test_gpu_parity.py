@@ -250,6 +250,30 @@ def test_lane_runs_at_the_stream_end(cuda_device, bits, shift):
         assert (host[:shift] == 0xAB).all() and (host[shift + ref_flat.size:] == 0xAB).all()
 
 
+def test_plan_cache_eviction_keeps_results(cuda_device):
+    """300 distinct non-dense layouts (each uploads its plane table; the
+    cache drops every plan after 256 uploads) interleaved with dense ones,
+    each unpacked and checked; the first layout is used again at the end."""
+    rng = np.random.default_rng(77)
+    H, C, bits = 1, 32, 8
+    cases = []
+    for k in range(300):
+        T = 16 * (k + 1)
+        reordered = np.asarray([[0, 1, 16, 32, 0, T], [0, 1, 0, 16, 0, T]], np.int64)
+        cases.append((T, reordered))
+        if k % 5 == 0:
+            cases.append((T, reordered[::-1].copy()))  # dense order
+    cases.append(cases[1])
+    for T, specs in cases:
+        sym = rng.integers(0, 256, T * H * C, dtype=np.uint8)
+        ref_flat, offs = oracle.pack_canonical(sym, bits, specs, [T, H, C], [0, 1, 2, -1])
+        lay = CanonicalLayout.make([T, H, C], ["token", "head", "head_dim"], bits, specs)
+        out = native_gpu.unpack_layout(_gpu_u8(ref_flat, cuda_device), lay)
+        assert np.array_equal(out.cpu().numpy(), sym), (T, specs.tolist())
+        flat = native_gpu.pack_layout(_gpu_u8(sym, cuda_device), lay)
+        assert np.array_equal(flat.cpu().numpy(), ref_flat), (T, specs.tolist())
+
+
 def test_irregular_plan_restore_falls_back_and_matches(cuda_device):
     rng = np.random.default_rng(5)
     tokens, H, C, bs = 300, 2, 32, 16
