@@ -97,10 +97,16 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+_entry_points: dict = {}
+
+
 def call(name: str, *args) -> int:
     """Calls an entry point; raises OrigamiNativeError on a non-zero status."""
     L = lib()
-    rc = getattr(L, name)(*args)
+    fn = _entry_points.get((id(L), name))
+    if fn is None:
+        fn = _entry_points[(id(L), name)] = getattr(L, name)
+    rc = fn(*args)
     if rc != ORIGAMI_OK:
         msg = L.origami_last_error().decode(errors="replace")
         raise OrigamiNativeError(rc, msg)

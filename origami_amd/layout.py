@@ -9,7 +9,7 @@ from the device.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from functools import lru_cache
+from functools import cached_property, lru_cache
 from typing import Iterable, Sequence
 
 import numpy as np
@@ -113,6 +113,15 @@ class CanonicalLayout:
     @property
     def num_chunks(self) -> int:
         return int(self.specs.shape[0])
+
+    @cached_property
+    def native_args(self) -> tuple[int, int, int, int]:
+        """(offsets, bits, specs) host addresses and the chunk count, as the
+        C entry points take them; the arrays live as long as the layout."""
+        for a in (self.offsets, self.bits, self.specs):
+            assert a.flags.c_contiguous and a.dtype == np.int64
+        return (self.offsets.ctypes.data, self.bits.ctypes.data, self.specs.ctypes.data,
+                int(self.specs.shape[0]))
 
     @property
     def stream_bytes(self) -> int:

@@ -12,6 +12,7 @@ on the host: no call reads device memory back.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from functools import lru_cache
 from typing import Any, Iterable, Sequence
@@ -26,8 +27,22 @@ CACHE_KV_FIRST = _native.CACHE_KV_FIRST
 CACHE_BLOCKS_FIRST = _native.CACHE_BLOCKS_FIRST
 
 
-def _stream_handle(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream_handle(device: torch.device):
+    """The calling thread's current stream on `device`, as a raw handle."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(index))
+    return ctypes.c_void_p(torch.cuda.current_stream(index).cuda_stream)
+
+
+def _device_guard(device: torch.device):
+    """Makes `device` current for the call (a no-op when it already is)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def _require_cuda(t: torch.Tensor, name: str) -> None:
@@ -73,10 +88,7 @@ def flat_chunks_and_offsets(chunks: Iterable[torch.Tensor] | torch.Tensor,
 
 
 def _layout_args(layout: CanonicalLayout) -> tuple:
-    return (
-        _native.host_ptr(layout.offsets), _native.host_ptr(layout.bits),
-        _native.host_ptr(layout.specs), layout.num_chunks,
-    )
+    return layout.native_args
 
 
 # ---------------------------------------------------------------------------
@@ -92,7 +104,7 @@ def unpack_layout(flat: torch.Tensor, layout: CanonicalLayout,
     if out is None:
         out = torch.empty((layout.symbol_count,), dtype=torch.uint8, device=flat.device)
     _require_cuda(out, "output")
-    with torch.cuda.device(flat.device):
+    with _device_guard(flat.device):
         _native.call(
             "origami_unpack_canonical_storage_chunks",
             flat.data_ptr(), flat.numel(), *_layout_args(layout),
@@ -111,7 +123,7 @@ def pack_layout(symbols: torch.Tensor, layout: CanonicalLayout,
     if out is None:
         out = torch.empty((layout.stream_bytes,), dtype=torch.uint8, device=symbols.device)
     _require_cuda(out, "flat_chunks")
-    with torch.cuda.device(symbols.device):
+    with _device_guard(symbols.device):
         _native.call(
             "origami_pack_canonical_storage_chunks",
             symbols.data_ptr(), symbols.numel(), *_layout_args(layout),
@@ -229,7 +241,7 @@ def unpack_to_kv_cache(flat: torch.Tensor, layout: CanonicalLayout, tokens: int,
     code, nb, bs, H, head_bytes = cache_geometry(kv_cache)
     if layout.token_count != 2 * tokens or layout.num_heads != H or layout.head_dim != head_bytes:
         raise RuntimeError("symbol layout does not match the kv_cache geometry")
-    with torch.cuda.device(kv_cache.device):
+    with _device_guard(kv_cache.device):
         try:
             _native.call(
                 "origami_unpack_canonical_to_kv_cache",
@@ -267,7 +279,7 @@ def pack_from_kv_cache(kv_cache: torch.Tensor, block_ids: torch.Tensor, tokens: 
         raise RuntimeError("symbol layout does not match the kv_cache geometry")
     if out is None:
         out = torch.empty((layout.stream_bytes,), dtype=torch.uint8, device=kv_cache.device)
-    with torch.cuda.device(kv_cache.device):
+    with _device_guard(kv_cache.device):
         try:
             _native.call(
                 "origami_pack_canonical_from_kv_cache",
@@ -306,7 +318,7 @@ def scatter_kv_blocks(value: torch.Tensor, tokens: int, kv_cache: torch.Tensor,
     code, nb, bs, H, head_bytes = cache_geometry(kv_cache)
     if value.numel() * value.element_size() != 2 * tokens * H * head_bytes:
         raise RuntimeError("value size does not match 2 * tokens * heads * head_dim")
-    with torch.cuda.device(kv_cache.device):
+    with _device_guard(kv_cache.device):
         _native.call("origami_scatter_kv_blocks", value.data_ptr(), int(tokens),
                      kv_cache.data_ptr(), code, nb, bs, H, head_bytes,
                      block_ids.data_ptr(), block_ids.numel(), _stream_handle(kv_cache.device))
@@ -321,7 +333,7 @@ def gather_kv_blocks(kv_cache: torch.Tensor, block_ids: torch.Tensor,
     n = 2 * block_ids.numel() * bs * H * head_bytes
     if out is None:
         out = torch.empty((n,), dtype=torch.uint8, device=kv_cache.device)
-    with torch.cuda.device(kv_cache.device):
+    with _device_guard(kv_cache.device):
         _native.call("origami_gather_kv_blocks", kv_cache.data_ptr(), code, nb, bs, H,
                      head_bytes, block_ids.data_ptr(), block_ids.numel(), out.data_ptr(),
                      _stream_handle(kv_cache.device))
@@ -392,7 +404,7 @@ def cachegen_unpack_dequantize_to_kv_cache(
     max_code = _max_tensors(max_key, max_value)
     ids = block_ids.to(device=kv_cache.device, dtype=torch.int64).contiguous()
     code, nb, bs = dequant_cache_geometry(kv_cache, heads, head_dim)
-    with torch.cuda.device(kv_cache.device):
+    with _device_guard(kv_cache.device):
         _native.call(
             "origami_cachegen_unpack_dequantize_to_kv_cache",
             flat.data_ptr(), flat.numel(), int(key_offset), int(key_bytes), int(value_offset),
@@ -438,7 +450,7 @@ def cachegen_unpack_dequantize(
     max_code = _max_tensors(max_key, max_value)
     out = torch.empty((layers, 2, int(heads), int(tokens), int(head_dim)), dtype=torch.float16,
                       device=flat.device)
-    with torch.cuda.device(flat.device):
+    with _device_guard(flat.device):
         _native.call(
             "origami_cachegen_unpack_dequantize",
             flat.data_ptr(), flat.numel(), _native.host_ptr(offs), _native.host_ptr(bits),
@@ -490,7 +502,7 @@ def kivi_dequantize_to_kv_cache(
     counts = _native.i64_array([t.numel() for t in metas])
     ids = block_ids.to(device=kv_cache.device, dtype=torch.int64).contiguous()
     code, nb, bs = dequant_cache_geometry(kv_cache, heads, head_dim)
-    with torch.cuda.device(kv_cache.device):
+    with _device_guard(kv_cache.device):
         _native.call(
             "origami_kivi_dequantize_to_kv_cache",
             flat.data_ptr(), flat.numel(), int(key_offset), int(key_bytes), int(value_offset),
