@@ -11,14 +11,14 @@
 //
 // Kernel design (wave64, 16-byte lanes):
 //  * rows kernels (the hot path).  A lane owns a 16-channel x 16-token byte
-//    tile.  It reads the 16 planes' 16-token runs (one 16-byte load each when
-//    b = 8 and aligned), transposes the 16x16 bytes in registers with
-//    v_perm_b32, and writes 16 destination rows of 16 bytes.  Eight lanes
-//    share a channel group and cover 128 consecutive tokens (a full 128-byte
-//    line of a plane per load instruction); eight lanes share a token and
-//    cover 128 consecutive channels (a full 128-byte line of a destination
-//    row per store instruction).  No LDS is needed for the data; LDS holds
-//    only the 128 plane descriptors a workgroup shares.
+//    tile.  It reads the 16 planes' 16-token runs (2b bytes each: one vector
+//    load per run, see RowsMode), transposes the 16x16 bytes in registers
+//    with v_perm_b32, and writes 16 destination rows of 16 bytes.  Eight
+//    lanes share a channel group and cover 128 consecutive tokens (a full
+//    128-byte line of a plane per load instruction at b = 8); eight lanes
+//    share a token and cover 128 consecutive channels (a full 128-byte line
+//    of a destination row per store instruction).  No LDS is needed for the
+//    data; LDS holds only the plane descriptors a workgroup shares.
 //  * generic kernels: one thread per symbol / per output byte, for layouts the
 //    rows kernels do not serve (irregular chunk plans, channel-major layouts).
 #include <hip/hip_runtime.h>
@@ -26,8 +26,8 @@
 #include <stdint.h>
 
 #include <algorithm>
-#include <cstring>
 #include <atomic>
+#include <cstring>
 #include <memory>
 #include <mutex>
 #include <string>
