@@ -246,8 +246,8 @@ struct Plan {
   ~Plan() {
     if (dev) (void)hipFree(dev);  // hipFree waits for work still reading it
   }
-  std::vector<int64_t> key;
   int device = -1;
+  bool want_table = false;
   int64_t n = 0, T = 0, H = 0, C = 0, max_symbols = 0;
   PlanInfo info;
   bool has_table = false;    // info was computed (row-kernel layout)
@@ -265,14 +265,28 @@ size_t g_plan_count = 0;         // plans in the cache
 size_t g_plan_device_count = 0;  // of which hold device memory
 constexpr size_t kMaxHostPlans = 4096;
 
-uint64_t hash_words(const std::vector<int64_t>& w) {
-  uint64_t h = 1469598103934665603ull;
-  for (int64_t v : w) {
-    h ^= static_cast<uint64_t>(v);
+uint64_t hash_words(uint64_t h, const int64_t* w, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    h ^= static_cast<uint64_t>(w[i]);
     h *= 1099511628211ull;
     h ^= h >> 29;
   }
   return h;
+}
+
+// True when `plan` was built from exactly this metadata (its host copy holds
+// offsets | bits | specs).
+bool plan_matches(const Plan& plan, const int64_t* offsets, const int64_t* bits,
+                  const int64_t* specs, int64_t n, int64_t T, int64_t H, int64_t C,
+                  int device, bool want_table) {
+  if (plan.n != n || plan.T != T || plan.H != H || plan.C != C || plan.device != device ||
+      plan.want_table != want_table)
+    return false;
+  const int64_t* h = plan.host.data();
+  const size_t w = sizeof(int64_t);
+  return std::memcmp(h, offsets, (n + 1) * w) == 0 &&
+         std::memcmp(h + (n + 1), bits, n * w) == 0 &&
+         std::memcmp(h + (n + 1) + n, specs, 6 * n * w) == 0;
 }
 
 void drop_all_plans() {
@@ -322,24 +336,17 @@ int get_plan(const int64_t* offsets, const int64_t* bits, const int64_t* specs,
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess)
     return fail(ORIGAMI_ERR_HIP, "hipGetDevice failed");
-  std::vector<int64_t> key;
-  key.reserve(static_cast<size_t>(8 * n + 8));
-  key.push_back(n);
-  key.push_back(T);
-  key.push_back(H);
-  key.push_back(C);
-  key.push_back(device);
-  key.push_back(want_table ? 1 : 0);
-  key.insert(key.end(), offsets, offsets + n + 1);
-  key.insert(key.end(), bits, bits + n);
-  key.insert(key.end(), specs, specs + 6 * n);
-  const uint64_t h = hash_words(key);
+  const int64_t dims[6] = {n, T, H, C, device, want_table ? 1 : 0};
+  uint64_t h = hash_words(1469598103934665603ull, dims, 6);
+  h = hash_words(h, offsets, n + 1);
+  h = hash_words(h, bits, n);
+  h = hash_words(h, specs, 6 * n);
 
   std::lock_guard<std::mutex> lock(g_plan_mutex);
   auto it = g_plans.find(h);
   if (it != g_plans.end()) {
     for (auto& p : it->second) {
-      if (p->key == key) {
+      if (plan_matches(*p, offsets, bits, specs, n, T, H, C, device, want_table)) {
         *out = p;
         return ORIGAMI_OK;
       }
@@ -348,7 +355,7 @@ int get_plan(const int64_t* offsets, const int64_t* bits, const int64_t* specs,
   if (g_plan_device_count >= kMaxPlans || g_plan_count >= kMaxHostPlans) drop_all_plans();
 
   auto plan = std::make_shared<Plan>();
-  plan->key = key;
+  plan->want_table = want_table;
   plan->device = device;
   plan->n = n;
   plan->T = T;
