@@ -1,5 +1,6 @@
 """Seeded random restores and saves through the fused paged-cache entry points,
-each compared byte for byte with the oracle.
+and seeded random CacheGen / KIVI dequantizing restores, each compared bit for
+bit with the oracle.
 
 Every case draws a token count (ragged or a multiple of 16), heads, head
 bytes, symbol width, block size, cache layout, a permuted block table, a
@@ -120,3 +121,54 @@ def test_random_storage_unpack_and_pack(cuda_device, seed):
     host = dst.cpu().numpy()
     assert np.array_equal(host[shift:shift + flat.size], flat), case
     assert (host[:shift] == 0xCD).all() and (host[shift + flat.size:] == 0xCD).all(), case
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_random_cachegen_restore(cuda_device, seed):
+    from tests.test_gpu_dequant import _run_both
+
+    rng = np.random.default_rng(7000 + seed)
+    heads = int(rng.integers(1, 9))
+    head_dim = 8 * int(rng.integers(1, 33)) if seed % 3 else int(rng.integers(1, 70))
+    tokens = int(rng.integers(1, 2000))
+    bs = int(rng.choice([8, 16, 32]))
+    nblk = -(-tokens // bs)
+    nb = nblk + int(rng.integers(0, 6))
+    kbits, vbits = int(rng.integers(2, 9)), int(rng.integers(2, 9))
+    kbins = int(rng.integers(4, (1 << kbits) + 1))
+    vbins = int(rng.integers(4, (1 << vbits) + 1))
+    case = dict(tokens=tokens, heads=heads, head_dim=head_dim, bs=bs, nb=nb,
+                ids=rng.permutation(nb)[:nblk].tolist(), key_bits=kbits, value_bits=vbits,
+                key_bins=kbins, value_bins=vbins,
+                out_dtype=[torch.float16, torch.bfloat16][seed % 2],
+                max_dtype=[np.float16, np.float32][(seed // 2) % 2],
+                blocks_first=bool(rng.integers(0, 2)), gap=int(rng.integers(0, 6)),
+                cache_offset=int(rng.choice([0, 0, 0, 1])))
+    got, expect = _run_both(cuda_device, rng, **case)
+    assert np.array_equal(got, expect), {k: v for k, v in case.items() if k != "ids"}
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_random_kivi_restore(cuda_device, seed):
+    from tests.test_gpu_dequant import _kivi_run_both
+
+    rng = np.random.default_rng(9000 + seed)
+    heads = int(rng.integers(1, 9))
+    head_dim = 8 * int(rng.integers(1, 33)) if seed % 3 else int(rng.integers(1, 70))
+    tokens = int(rng.integers(1, 1500))
+    sink = int(min(tokens, rng.choice([0, 16, 24, 128])))
+    bits = int(rng.integers(1, 9))
+    nibble3 = bits == 3 and bool(rng.integers(0, 2))
+    group = int(rng.choice([16, 32, 64, 128])) if seed % 4 else int(rng.integers(1, 100))
+    bs = int(rng.choice([8, 16, 32]))
+    nblk = -(-tokens // bs)
+    nb = nblk + int(rng.integers(0, 6))
+    case = dict(tokens=tokens, sink=sink, heads=heads, head_dim=head_dim, bits=bits,
+                nibble3=nibble3, group=group, bs=bs, nb=nb,
+                ids=rng.permutation(nb)[:nblk].tolist(),
+                out_dtype=[torch.float16, torch.bfloat16][seed % 2],
+                meta_dtype=[np.float16, np.float32][(seed // 2) % 2],
+                blocks_first=bool(rng.integers(0, 2)), gap=int(rng.integers(0, 6)),
+                cache_offset=int(rng.choice([0, 0, 0, 1])))
+    got, expect = _kivi_run_both(cuda_device, rng, **case)
+    assert np.array_equal(got, expect), {k: v for k, v in case.items() if k != "ids"}
