@@ -274,6 +274,53 @@ def test_plan_cache_eviction_keeps_results(cuda_device):
         assert np.array_equal(flat.cpu().numpy(), ref_flat), (T, specs.tolist())
 
 
+def test_concurrent_restores_from_threads(cuda_device):
+    """Four threads, each on its own stream, restore and re-pack layers with
+    dense and reordered plans (plans created and uploaded concurrently)."""
+    import threading
+
+    errors = []
+
+    def worker(tid):
+        try:
+            rng = np.random.default_rng(900 + tid)
+            stream = torch.cuda.Stream(device=cuda_device)
+            with torch.cuda.stream(stream):
+                for it in range(12):
+                    tokens = 16 * int(rng.integers(4, 40)) + (it % 2) * 5
+                    H, C, bs = 2, 64, 16
+                    specs = planner_specs(2 * tokens, H, C, 1 << 12)
+                    if (tid + it) % 2:
+                        specs = specs[::-1].copy()
+                    value = rng.integers(0, 256, (2, tokens, H, C), dtype=np.uint8)
+                    flat, offs = oracle.pack_canonical(value.reshape(-1), 8, specs,
+                                                       [2 * tokens, H, C], [0, 1, 2, -1])
+                    ids, cache = _kv_case(rng, tokens, H, C, bs, bool(it % 3 == 0))
+                    expect = cache.copy()
+                    oracle.restore_layer(flat, offs, 8, specs, tokens, H, C, ids, expect,
+                                         bool(it % 3 == 0))
+                    cache_gpu = _gpu_u8(cache, cuda_device)
+                    lay = kv_symbol_layout(tokens, H, C, 8, specs)
+                    ids_gpu = native_gpu.block_ids_tensor(ids, cuda_device)
+                    native_gpu.unpack_to_kv_cache(_gpu_u8(flat, cuda_device), lay, tokens,
+                                                  cache_gpu, ids_gpu)
+                    back = native_gpu.pack_from_kv_cache(cache_gpu, ids_gpu, tokens, lay)
+                    stream.synchronize()
+                    if not np.array_equal(cache_gpu.cpu().numpy(), expect):
+                        errors.append((tid, it, "restore"))
+                    if not np.array_equal(back.cpu().numpy(), flat):
+                        errors.append((tid, it, "save"))
+        except Exception as exc:  # noqa: BLE001 - reported below
+            errors.append((tid, repr(exc)))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+
+
 def test_irregular_plan_restore_falls_back_and_matches(cuda_device):
     rng = np.random.default_rng(5)
     tokens, H, C, bs = 300, 2, 32, 16
