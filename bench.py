@@ -58,6 +58,9 @@ def parse_args():
                     help="skip the restore legs at the other KV geometries")
     ap.add_argument("--config-layers", type=int, default=4,
                     help="layers per geometry in the configs leg")
+    ap.add_argument("--no-connector", action="store_true",
+                    help="skip the end-to-end save/restore through the connector")
+    ap.add_argument("--connector-layers", type=int, default=8)
     ap.add_argument("--profile-only", action="store_true",
                     help="only the timed restore loop (for rocprofv3 runs)")
     ap.add_argument("--profile-dequant", action="store_true",
@@ -255,6 +258,9 @@ def main() -> int:
 
     if not args.no_configs:
         result["configs"] = configs_leg(dev, max(3, args.steps // 2), args.config_layers)
+
+    if not args.no_connector:
+        result["connector"] = connector_leg(dev, args.connector_layers, T, H, D, bs)
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(streams[0], layout, specs, T, H, C, bs, NB,
@@ -468,6 +474,86 @@ def configs_leg(dev, steps, layers):
     build("llama3-8b-fp8-16x16k", 8, 128, torch.float8_e4m3fn, [16384] * 16, 3, False)
     build("llama3-70b-128k", 8, 128, torch.bfloat16, [131072], 4, False)
     return out
+
+
+def connector_leg(dev, layers, T, H, D, bs):
+    """Save and restore `layers` layers of one T-token request end to end
+    through the connector (OrigamiConnector, worker role): raw_byte_planes
+    symbols, 1 MiB chunks, the zlib CPU codec on 16 threads, the in-memory
+    store.  Save: save_kv_layer for every layer, then wait_for_save (fused
+    gather + pack, device-to-host, compression).  Restore: start_load_kv,
+    then wait_for_layer_load for every layer (decompression into pinned
+    staging, host-to-device, fused unpack + scatter), to the last layer's
+    completion.  Rates are KV bytes (2 * T * H * D * 2 per layer) per second;
+    the restored caches are compared with the saved ones."""
+    import types
+
+    import torch
+
+    from origami_amd.connector import KVConnectorRole, OrigamiConnector
+    from origami_amd.metadata import (OrigamiConnectorMetadata, OrigamiRestoreRequest,
+                                      OrigamiSaveRequest)
+    from origami_amd.synthetic import fill_layer
+
+    def connector(ns):
+        cfg = types.SimpleNamespace(kv_transfer_config=types.SimpleNamespace(
+            kv_connector_extra_config={
+                "origami_quantizer": "raw_byte_planes", "origami_lossless_cpu_backend": "zlib",
+                "origami_store_uri": f"memory://{ns}", "origami_qat_threads": 16}))
+        return OrigamiConnector(cfg, KVConnectorRole.WORKER)
+
+    nblk = -(-T // bs)
+    NB = nblk + nblk // 4
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    names = [f"model.layers.{i}.self_attn.attn" for i in range(layers)]
+    src, dst = {}, {}
+    for n in names:
+        src[n] = torch.zeros((2, NB, bs, H, D), dtype=torch.bfloat16, device=dev)
+        fill_layer(src[n], torch.arange(NB, device=dev), gen)
+        dst[n] = torch.zeros_like(src[n])
+    src_ids = torch.randperm(NB, generator=gen, device=dev)[:nblk].tolist()
+    dst_ids = torch.randperm(NB, generator=gen, device=dev)[:nblk].tolist()
+    kv_bytes = layers * 2 * T * H * D * 2
+
+    saver = connector("bench-connector")
+    saver.register_kv_caches(src)
+    saver.bind_connector_metadata(OrigamiConnectorMetadata(reqs_to_save={
+        "s": OrigamiSaveRequest(request_id="s", cache_key="bench", block_ids_per_group=(
+            tuple(src_ids),), num_tokens=T)}))
+    saver.start_load_kv(None)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for n in names:
+        saver.save_kv_layer(n, src[n], None)
+    saver.wait_for_save()
+    save_s = time.perf_counter() - t0
+    payload = saver.store.get("bench")
+    stored = sum(int(c.compressed.numel()) for lp in payload.layer_payloads.values()
+                 for c in lp.chunks)
+
+    loader = connector("bench-connector")  # same in-memory store namespace
+    loader.register_kv_caches(dst)
+    loader.bind_connector_metadata(OrigamiConnectorMetadata(reqs_to_restore={
+        "r": OrigamiRestoreRequest(request_id="r", cache_key="bench", block_ids_per_group=(
+            tuple(dst_ids),), num_tokens=T)}))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    loader.start_load_kv(None)
+    for n in names:
+        loader.wait_for_layer_load(n)
+    torch.cuda.synchronize()
+    restore_s = time.perf_counter() - t0
+    ok = all(torch.equal(dst[n][:, dst_ids].view(torch.int16), src[n][:, src_ids].view(torch.int16))
+             for n in names[:2])
+    return {
+        "layers": layers, "tokens": T, "codec": "zlib level 1, 16 threads",
+        "kv_bytes": kv_bytes, "stored_bytes": stored,
+        "save_ms": round(save_s * 1e3, 2), "save_gbps": round(kv_bytes / save_s / 1e9, 3),
+        "restore_ms": round(restore_s * 1e3, 2),
+        "restore_gbps": round(kv_bytes / restore_s / 1e9, 3),
+        "restore_ok": ok,
+    }
 
 
 def pipeline_leg(streams, layout, T, dst_caches, dst_ids, dev, kernel_ms):

@@ -4,18 +4,27 @@ Backends: "zlib" (raw DEFLATE, level 1, wbits -15, as cpu_qat.py:64-83) and
 "raw" (identity).  Intel QAT ("qat") is outside this build: requesting it
 raises unless allow_zlib_fallback is set, which is the reference's behaviour
 on a host without QAT devices (cpu_qat.py:41-55).
+
+Chunks are independent, so with threads > 1 the zlib backend compresses and
+decompresses them on a thread pool (zlib releases the GIL); the output order
+and bytes do not depend on the thread count.
 """
 from __future__ import annotations
 
 import zlib
+from concurrent.futures import ThreadPoolExecutor
 
+import numpy as np
 import torch
 
 
 class CpuLosslessCodec:
-    def __init__(self, backend: str = "qat", allow_zlib_fallback: bool = False, **_unused):
+    def __init__(self, backend: str = "qat", allow_zlib_fallback: bool = False,
+                 threads: int = 1, **_unused):
         self.backend = backend
         self.allow_zlib_fallback = allow_zlib_fallback
+        self.threads = max(1, int(threads))
+        self._pool = ThreadPoolExecutor(max_workers=self.threads) if self.threads > 1 else None
         if backend == "qat":
             if not allow_zlib_fallback:
                 raise RuntimeError(
@@ -33,22 +42,30 @@ class CpuLosslessCodec:
     @staticmethod
     def _zlib_compress(data: torch.Tensor) -> torch.Tensor:
         comp = zlib.compressobj(level=1, wbits=-15, strategy=zlib.Z_DEFAULT_STRATEGY)
-        raw = CpuLosslessCodec._cpu_u8(data).numpy().tobytes()
-        out = comp.compress(raw) + comp.flush()
-        return torch.frombuffer(bytearray(out), dtype=torch.uint8).clone()
+        view = memoryview(CpuLosslessCodec._cpu_u8(data).numpy())  # no copy
+        out = comp.compress(view) + comp.flush()
+        return torch.from_numpy(np.frombuffer(out, dtype=np.uint8).copy())
 
     @staticmethod
     def _zlib_decompress_into(data: torch.Tensor, out: torch.Tensor) -> None:
-        raw = zlib.decompress(CpuLosslessCodec._cpu_u8(data).numpy().tobytes(), wbits=-15)
+        raw = zlib.decompress(memoryview(CpuLosslessCodec._cpu_u8(data).numpy()), wbits=-15)
         if len(raw) != int(out.numel()):
             raise RuntimeError(
                 f"Origami CPU lossless decoded {len(raw)} bytes, expected {int(out.numel())}")
-        out.copy_(torch.frombuffer(bytearray(raw), dtype=torch.uint8))
+        out.numpy()[:] = np.frombuffer(raw, dtype=np.uint8)
+
+    def _map(self, fn, *iterables) -> list:
+        """fn over the chunks; on the pool for zlib (plain copies of the raw
+        backend are faster on the calling thread than handed to a pool)."""
+        items = list(zip(*iterables))
+        if self._pool is None or len(items) < 2 or self.backend == "raw":
+            return [fn(*a) for a in items]
+        return list(self._pool.map(lambda a: fn(*a), items))
 
     def compress_many(self, chunks) -> list[torch.Tensor]:
         if self.backend == "raw":
-            return [self._cpu_u8(c) for c in chunks]
-        return [self._zlib_compress(c) for c in chunks]
+            return self._map(self._cpu_u8, chunks)
+        return self._map(self._zlib_compress, chunks)
 
     def decompress_many(self, chunks, output_bytes) -> list[torch.Tensor]:
         if len(chunks) != len(output_bytes):
@@ -60,16 +77,19 @@ class CpuLosslessCodec:
     def decompress_into(self, chunks, outs: list[torch.Tensor]) -> None:
         """Decodes each chunk straight into a caller buffer (e.g. a slice of a
         pinned staging buffer), avoiding an intermediate copy."""
-        for chunk, out in zip(chunks, outs):
-            if self.backend == "raw":
-                flat = self._cpu_u8(chunk)
-                if int(flat.numel()) != int(out.numel()):
-                    raise RuntimeError(
-                        "Origami raw backend received "
-                        f"{int(flat.numel())} bytes, expected {int(out.numel())}")
-                out.copy_(flat)
-            else:
-                self._zlib_decompress_into(chunk, out)
+        if len(chunks) != len(outs):
+            raise ValueError("chunks and outputs must have the same length")
+        self._map(self._raw_into if self.backend == "raw" else self._zlib_decompress_into,
+                  chunks, outs)
+
+    @classmethod
+    def _raw_into(cls, chunk: torch.Tensor, out: torch.Tensor) -> None:
+        flat = cls._cpu_u8(chunk)
+        if int(flat.numel()) != int(out.numel()):
+            raise RuntimeError(
+                "Origami raw backend received "
+                f"{int(flat.numel())} bytes, expected {int(out.numel())}")
+        out.copy_(flat)
 
     def compress(self, data: torch.Tensor) -> torch.Tensor:
         return self.compress_many([data])[0]

@@ -100,7 +100,8 @@ class OrigamiConnectorWorker:
         self.quantizer: QuantizerAdapter = create_quantizer_adapter(
             config.quantizer, config.quantizer_config)
         self.cpu_codec = CpuLosslessCodec(backend=config.lossless_cpu_backend,
-                                          allow_zlib_fallback=config.allow_zlib_fallback)
+                                          allow_zlib_fallback=config.allow_zlib_fallback,
+                                          threads=config.qat_threads)
         self.kv_caches: dict[str, torch.Tensor] = {}
         self.layer_to_cache_group: dict[str, int] = {}
         self._executor = ThreadPoolExecutor(max_workers=max(1, config.qat_threads))

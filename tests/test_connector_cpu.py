@@ -111,3 +111,17 @@ def test_unknown_cache_key_fails_through_futures():
         conn.get_finished(set())
     with pytest.raises(NotImplementedError):
         conn.build_connector_meta(None)
+
+
+def test_codec_threads_give_the_same_bytes():
+    torch.manual_seed(3)
+    data = [torch.randint(0, 8, (int(n),), dtype=torch.uint8) for n in (70000, 1, 5000, 0, 123457)]
+    one = CpuLosslessCodec(backend="zlib", threads=1)
+    many = CpuLosslessCodec(backend="zlib", threads=4)
+    a, b = one.compress_many(data), many.compress_many(data)
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+    outs = [torch.empty(int(d.numel()), dtype=torch.uint8) for d in data]
+    many.decompress_into(b, outs)
+    assert all(torch.equal(x, y) for x, y in zip(outs, data))
+    with pytest.raises(RuntimeError, match="decoded"):
+        many.decompress_into(b[:2], [torch.empty(5, dtype=torch.uint8), outs[1]])
