@@ -103,10 +103,10 @@ _entry_points: dict = {}
 def call(name: str, *args) -> int:
     """Calls an entry point; raises OrigamiNativeError on a non-zero status."""
     L = lib()
-    fn = _entry_points.get((id(L), name))
-    if fn is None:
-        fn = _entry_points[(id(L), name)] = getattr(L, name)
-    rc = fn(*args)
+    entry = _entry_points.get(name)
+    if entry is None or entry[0] is not L:  # first call, or the library was reloaded
+        entry = _entry_points[name] = (L, getattr(L, name))
+    rc = entry[1](*args)
     if rc != ORIGAMI_OK:
         msg = L.origami_last_error().decode(errors="replace")
         raise OrigamiNativeError(rc, msg)

@@ -327,10 +327,10 @@ __global__ __launch_bounds__(kDqThreads) void cachegen_dense_generic_kernel(
 // along channels (scale[bt][c / group]); value = fmaf(s, scale, zero).
 //
 // Row kernel (C and head_dim multiples of 8, group a multiple of 16, block
-// size >= 16): a lane owns 8 channels x LT body tokens (LT = 16, or 32 at odd
-// widths, so that its run of one plane is whole dwords).  It reads that run
-// of each of its 8 planes with dword loads (funnel-shifted when the plane
-// does not start on a dword), keeps it packed, and for every token extracts
+// size >= 16): a lane owns 8 channels x LT body tokens (LT = 8 at widths up
+// to 2 bits, else 16).  It reads its run of each of its 8 planes with dword
+// loads (funnel-shifted when the run does not start on a dword), keeps it
+// packed, and for every token extracts
 // the 8 symbols, dequantizes them and writes one 16-byte store.  Eight lanes
 // along channels cover a 128-byte line of a destination row; eight lanes
 // along tokens read 8 * LT consecutive tokens of a plane.  A workgroup (2
@@ -342,11 +342,12 @@ constexpr int kKiviThreads = 64 * kKiviWavesC;
 constexpr int kKiviTileChannels = 64 * kKiviWavesC;
 constexpr int kKiviMaxGroups = kKiviTileChannels / 16;  // value groups per tile (group >= 16)
 
-// Body tokens per lane at `sbits` stored bits per symbol: the fewest that
-// make a lane's plane run whole dwords (LT * sbits a multiple of 32).  More
-// tokens per lane read longer runs but leave fewer waves to hide latency,
-// which measured slower.
-constexpr int kivi_lane_tokens(int sbits) { return sbits % 2 == 1 ? 32 : 16; }
+// Body tokens per lane at `sbits` stored bits per symbol.  Fewer tokens per
+// lane means more waves and shorter store bursts; more means longer plane
+// runs.  Measured on a 32768-token Llama-3-8B layer: 16 tokens rather than 32
+// at b = 3 (37.5-41.4 us against 48.0-48.2); 8 rather than 16 at b = 2 is
+// within run-to-run variation.
+constexpr int kivi_lane_tokens(int sbits) { return sbits <= 2 ? 8 : 16; }
 
 struct KiviHalf {
   const uint8_t* sbase;  // 4-byte aligned base of the half's stream
@@ -402,7 +403,8 @@ __device__ __forceinline__ void kivi_sink_rows(const KiviParams& p, int half, in
 template <int SBITS, bool NIB3, bool BF16, bool META_HALF>
 __global__ __launch_bounds__(kKiviThreads) void kivi_cache_kernel(KiviParams p) {
   constexpr int LT = kivi_lane_tokens(SBITS);
-  constexpr int NU = LT * SBITS / 32;  // packed dwords of a lane's plane run
+  constexpr int NU = (LT * SBITS + 31) / 32;  // dwords holding a lane's plane run
+  constexpr int CH = LT < 16 ? LT : 16;        // tokens per store chunk
   constexpr int TILE_T = 8 * LT;
   constexpr uint32_t mask = NIB3 ? 0x7u : (1u << SBITS) - 1u;
   __shared__ float vmeta[2][kKiviMaxGroups][TILE_T];
@@ -475,31 +477,31 @@ __global__ __launch_bounds__(kKiviThreads) void kivi_cache_kernel(KiviParams p) 
   const int gi = static_cast<int>(c0 / p.group - g_first);
   const int tt0 = static_cast<int>(bt0 - tile_bt0);
 
-  // 16-token chunks: each lies in one key group (group % 16 == 0) and in at
+  // CH-token chunks: each lies in one key group (group % 16 == 0) and in at
   // most two blocks (block_size >= 16).
 #pragma unroll
-  for (int jb = 0; jb < LT / 16; ++jb) {
-    if (16 * jb >= nj) break;
+  for (int jb = 0; jb < LT / CH; ++jb) {
+    if (CH * jb >= nj) break;
     float ks[8] = {}, kz[8] = {};
     if (half == 0) {
-      const int64_t g = (bt0 + 16 * jb) / p.group;
+      const int64_t g = (bt0 + CH * jb) / p.group;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         ks[i] = load_meta<META_HALF>(hs.scale, g * p.C + c0 + i);
         kz[i] = load_meta<META_HALF>(hs.zero, g * p.C + c0 + i);
       }
     }
-    const int64_t t0 = p.sink + bt0 + 16 * jb;
+    const int64_t t0 = p.sink + bt0 + CH * jb;
     const int64_t blk0 = t0 / p.bs;
     const int64_t off0 = t0 - blk0 * p.bs;
-    const int jsplit = static_cast<int>(min<int64_t>(16, p.bs - off0));
+    const int jsplit = static_cast<int>(min<int64_t>(CH, p.bs - off0));
     const int64_t row_a = kivi_row(p, half, blk0, off0);
-    const int64_t row_b = jsplit < nj - 16 * jb ? kivi_row(p, half, blk0 + 1, 0) : -1;
+    const int64_t row_b = jsplit < nj - CH * jb ? kivi_row(p, half, blk0 + 1, 0) : -1;
     uint16_t* const dst_a = p.cache + row_a * p.C + c0;
     uint16_t* const dst_b = p.cache + row_b * p.C + c0;
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      const int j = 16 * jb + jj;
+    for (int jj = 0; jj < CH; ++jj) {
+      const int j = CH * jb + jj;
       const bool second = jj >= jsplit;
       if (j < nj && (second ? row_b : row_a) >= 0) {
         uint32_t o[4];
