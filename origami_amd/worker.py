@@ -52,7 +52,7 @@ from origami_amd.metadata import (
 )
 from origami_amd.quantization import QuantizerAdapter, create_quantizer_adapter
 from origami_amd.quantization.raw_tensor import RawBytePlanesAdapter
-from origami_amd.restore_pipeline import LayerRestorePipeline
+from origami_amd.restore_pipeline import LayerRestorePipeline, LayerTiming, PipelineRegistry
 from origami_amd.store import OrigamiStore
 
 _NATIVE_LAYOUT_KEY = "origami_native_layout"
@@ -78,8 +78,20 @@ def _config_hash(config: dict[str, Any]) -> str:
 @dataclass
 class _LayerLoadResult:
     event: torch.cuda.Event | None = None
+    # (metric type, restore, layer payload, fields) rows whose fields hold
+    # "_cuda_start_event"/"_cuda_end_event"; read out after the layer's wait
     pending_metrics: list | None = None
     wait_on_current_stream: bool = True
+
+
+def _ms_since(start: float) -> float:
+    return (time.perf_counter() - start) * 1000.0
+
+
+def _restore_metric_id(restore: OrigamiRestoreRequest | None) -> str:
+    if restore is None:
+        return ""
+    return str(restore.metric_request_id or restore.request_id)
 
 
 def _layout_to_spec(layout: ChunkLayout) -> list[int]:
@@ -112,8 +124,11 @@ class OrigamiConnectorWorker:
         self._save_futures: list[Future] = []
         self._save_payloads: dict[str, OrigamiPayload] = {}
         self._save_lock = Lock()
-        self._pipeline_lock = Lock()
-        self._pipelines: dict[int, LayerRestorePipeline] = {}
+        self._pipelines = PipelineRegistry(self._make_pipeline)
+        # CUDA-timed metric rows whose end event had not completed when their
+        # layer was waited on; written once it has (or at shutdown)
+        self._deferred_metrics: list = []
+        self._metrics_lock = Lock()
         self._metadata: OrigamiConnectorMetadata | None = None
         self.metrics_path = (str(Path(config.metrics_dir) / "origami_metrics.jsonl")
                              if config.metrics_dir else None)
@@ -133,17 +148,15 @@ class OrigamiConnectorWorker:
             mapping.setdefault(name, 0)
         self.layer_to_cache_group = mapping
 
-    def _pipeline(self, device: torch.device, slot_bytes: int) -> LayerRestorePipeline:
+    def _make_pipeline(self, index: int, slot_bytes: int) -> LayerRestorePipeline:
+        return LayerRestorePipeline(torch.device("cuda", index), slot_bytes,
+                                    num_slots=self.config.restore_slots)
+
+    def _lease_pipeline(self, device: torch.device, slot_bytes: int):
+        """Context manager holding the device's pipeline (slots of at least
+        slot_bytes) for one submit; a replaced pipeline outlives its leases."""
         index = device.index if device.index is not None else torch.cuda.current_device()
-        with self._pipeline_lock:
-            pipe = self._pipelines.get(index)
-            if pipe is None or pipe.slot_bytes < slot_bytes:
-                if pipe is not None:
-                    pipe.synchronize()
-                pipe = LayerRestorePipeline(torch.device("cuda", index), slot_bytes,
-                                            num_slots=self.config.restore_slots)
-                self._pipelines[index] = pipe
-            return pipe
+        return self._pipelines.lease(index, int(slot_bytes))
 
     # --------------------------------------------------------------- restore
 
@@ -175,12 +188,13 @@ class OrigamiConnectorWorker:
                 restore.cache_key, read_bandwidth_gbps=self.config.read_bandwidth_gbps,
                 metrics_path=self.metrics_path, request_id=restore.request_id,
                 system="origami")
+            start_perf = time.perf_counter()
             # layers are issued in model order (the kv_caches order)
             for layer_name, fut in layer_futures.items():
                 if fut.done():
                     continue
                 try:
-                    result = self._restore_layer(restore, payload, layer_name)
+                    result = self._restore_layer(restore, payload, layer_name, start_perf)
                 except Exception as exc:  # noqa: BLE001 - delivered through the future
                     fut.set_exception(exc)
                 else:
@@ -193,7 +207,8 @@ class OrigamiConnectorWorker:
             raise
 
     def _restore_layer(self, restore: OrigamiRestoreRequest, payload: OrigamiPayload,
-                       layer_name: str) -> _LayerLoadResult | None:
+                       layer_name: str, start_perf: float | None = None
+                       ) -> _LayerLoadResult | None:
         layer_payload = payload.layer_payloads.get(layer_name)
         if layer_payload is None or layer_name not in self.kv_caches:
             return None
@@ -217,45 +232,101 @@ class OrigamiConnectorWorker:
                                "payload chunks")
         _, nb, bs, H, head_bytes = native_gpu.cache_geometry(kv_cache)
         with nvtx_range("origami:restore_layer"):
+            result = None
             if fmt == "raw_byte_planes" and kv_cache.is_cuda:
-                return self._restore_byte_planes(layer_payload, layout, kv_cache, block_ids, bs,
-                                                 nb, meta)
-            if fmt == "raw_bytes" and kv_cache.is_cuda and self._raw_bytes_scatterable(
+                result = self._restore_byte_planes(restore, layer_payload, layout, kv_cache,
+                                                   block_ids, bs, nb, meta)
+            elif fmt == "raw_bytes" and kv_cache.is_cuda and self._raw_bytes_scatterable(
                     meta, kv_cache, layout):
-                return self._restore_raw_bytes(layer_payload, layout, kv_cache, block_ids, nb, meta)
-            if fmt in _FUSED_DEQUANT_FORMATS and kv_cache.is_cuda:
+                result = self._restore_raw_bytes(restore, layer_payload, layout, kv_cache,
+                                                 block_ids, nb, meta)
+            elif fmt in _FUSED_DEQUANT_FORMATS and kv_cache.is_cuda:
                 result = self._restore_fused_dequant(restore, layer_payload, layout, kv_cache,
                                                      block_ids, nb, meta)
-                if result is not None:
-                    return result
-            return self._restore_generic(restore, layer_payload, layout, kv_cache, block_ids)
+            if result is None:
+                result = self._restore_generic(restore, layer_payload, layout, kv_cache,
+                                               block_ids)
+        if start_perf is not None:
+            # host-side readiness of the layer: everything for it is enqueued
+            # (worker.py:1072-1080)
+            self._write_restore_metric("layer_ready", restore, layer_payload, {
+                "ms": _ms_since(start_perf), "chunks": len(layer_payload.chunks)})
+        return result
 
-    def _fill_from_chunks(self, layer_payload: LayerPayload, layout: CanonicalLayout):
+    def _fill_from_chunks(self, layer_payload: LayerPayload, layout: CanonicalLayout,
+                          timing: dict | None = None):
         sizes = layout.chunk_sizes()
         for rec, size in zip(layer_payload.chunks, sizes):
             if int(rec.unpacked_bytes) != size:
                 raise RuntimeError("Origami CUDA packed chunk byte size mismatch")
 
         def fill(staging: torch.Tensor) -> None:
+            start = time.perf_counter()
             off = layout.offsets
             outs = [staging[int(off[k]):int(off[k + 1])] for k in range(layout.num_chunks)]
             self.cpu_codec.decompress_into([r.compressed for r in layer_payload.chunks], outs)
+            if timing is not None:
+                timing["ms"] = _ms_since(start)
         return fill
 
-    def _restore_byte_planes(self, layer_payload, layout, kv_cache, block_ids, bs, nb, meta):
+    def _submit_layer(self, restore, layer_payload, layout, kv_cache, ids_dev, compute,
+                      metric_type: str, fields: dict[str, Any]) -> _LayerLoadResult:
+        """Decompress into pinned staging, then H2D + `compute` on the device
+        pipeline.  With metrics on, writes the layer's lossless_decompress row
+        and returns h2d_copy and `metric_type` rows timed by events, to be read
+        out after the layer's wait (worker.py:574-617)."""
+        timed = self.metrics_path is not None
+        fill_timing: dict | None = {} if timed else None
+        with self._lease_pipeline(kv_cache.device, layout.stream_bytes) as pipe:
+            ids_dev.record_stream(pipe.compute_stream)
+            out = pipe.submit(self._fill_from_chunks(layer_payload, layout, fill_timing),
+                              layout.stream_bytes, compute, timed=timed)
+        if not timed:
+            return _LayerLoadResult(event=out)
+        event, timing = out
+        compressed = sum(int(r.compressed_bytes) for r in layer_payload.chunks)
+        unpacked = int(layout.stream_bytes)
+        ms = float(fill_timing.get("ms", 0.0))
+        self._write_restore_metric("lossless_decompress", restore, layer_payload, {
+            "device": "cpu", "backend": self.cpu_codec.backend,
+            "chunks": len(layer_payload.chunks), "compressed_bytes": compressed,
+            "unpacked_bytes": unpacked, "ms": ms,
+            "compressed_gbps": compressed * 8.0 / ms / 1e6 if ms > 0 else 0.0,
+            "unpacked_gbps": unpacked * 8.0 / ms / 1e6 if ms > 0 else 0.0})
+        h2d = {"bytes_copied": unpacked, "bytes": unpacked, "start_ts": time.time(),
+               "device": str(kv_cache.device), "source_device": "cpu (pinned staging)",
+               "copy_kind": "dram_to_hbm", "copy_stream": True,
+               "_cuda_start_event": timing.h2d_start, "_cuda_end_event": timing.h2d_end}
+        row = {"chunks": len(layer_payload.chunks), "unpacked_bytes": unpacked,
+               "input_bytes": unpacked, **fields,
+               "_cuda_start_event": timing.compute_start, "_cuda_end_event": timing.compute_end}
+        pending = [("h2d_copy", restore, layer_payload, h2d),
+                   (metric_type, restore, layer_payload, row)]
+        return _LayerLoadResult(event=event, pending_metrics=pending)
+
+    @staticmethod
+    def _written_bytes(kv_cache: torch.Tensor, nblk: int) -> int:
+        """Bytes a restore writes into the cache: K and V of nblk whole blocks
+        ([bs, H, D] each in both cache layouts)."""
+        bs, H, D = (int(x) for x in kv_cache.shape[2:])
+        return 2 * nblk * bs * H * D * kv_cache.element_size()
+
+    def _restore_byte_planes(self, restore, layer_payload, layout, kv_cache, block_ids, bs, nb,
+                             meta):
         tokens = int(meta.get("token_count", layout.token_count // 2))
         if layout.token_count != 2 * tokens:
             raise RuntimeError("raw_byte_planes symbol token axis must be 2 * token_count")
         needed = -(-tokens // bs)
         if len(block_ids) < needed:
             raise RuntimeError("tokens exceed destination block capacity")
-        pipe = self._pipeline(kv_cache.device, layout.stream_bytes)
         ids_dev = native_gpu.block_ids_tensor(block_ids[:needed], kv_cache.device, nb)
-        ids_dev.record_stream(pipe.compute_stream)
-        event = pipe.submit(
-            self._fill_from_chunks(layer_payload, layout), layout.stream_bytes,
-            lambda flat: native_gpu.unpack_to_kv_cache(flat, layout, tokens, kv_cache, ids_dev))
-        return _LayerLoadResult(event=event)
+        written = self._written_bytes(kv_cache, needed)
+        return self._submit_layer(
+            restore, layer_payload, layout, kv_cache, ids_dev,
+            lambda flat: native_gpu.unpack_to_kv_cache(flat, layout, tokens, kv_cache, ids_dev),
+            "bitunpack_cuda",
+            {"backend": "hip_fused_unpack_scatter", "symbols": int(layout.symbol_count),
+             "output_bytes": written, "bytes": int(layout.stream_bytes) + written})
 
     @staticmethod
     def _raw_bytes_scatterable(meta, kv_cache, layout) -> bool:
@@ -265,20 +336,22 @@ class OrigamiConnectorWorker:
                 and dtype == str(kv_cache.dtype).replace("torch.", "")
                 and layout.shape[0] == 1 and layout.shape[1] == 1 and layout.uniform_bits == 8)
 
-    def _restore_raw_bytes(self, layer_payload, layout, kv_cache, block_ids, nb, meta):
+    def _restore_raw_bytes(self, restore, layer_payload, layout, kv_cache, block_ids, nb, meta):
         """Reference raw_bytes payload ([1, 1, N] bits 8 = the blocks' bytes in
         [2, nblk, bs, H, D] order): H2D + block scatter."""
         nblk = int(meta["shape"][1])
         if len(block_ids) < nblk:
             raise RuntimeError("tokens exceed destination block capacity")
         tokens = nblk * int(kv_cache.shape[2])
-        pipe = self._pipeline(kv_cache.device, layout.stream_bytes)
         ids_dev = native_gpu.block_ids_tensor(block_ids[:nblk], kv_cache.device, nb)
-        ids_dev.record_stream(pipe.compute_stream)
-        event = pipe.submit(
-            self._fill_from_chunks(layer_payload, layout), layout.stream_bytes,
-            lambda flat: native_gpu.scatter_kv_blocks(flat, tokens, kv_cache, ids_dev))
-        return _LayerLoadResult(event=event)
+        written = self._written_bytes(kv_cache, nblk)
+        return self._submit_layer(
+            restore, layer_payload, layout, kv_cache, ids_dev,
+            lambda flat: native_gpu.scatter_kv_blocks(flat, tokens, kv_cache, ids_dev),
+            "restore_materialize",
+            {"backend": "hip_block_scatter", "device": str(kv_cache.device),
+             "direct_to_kv_cache": True, "output_bytes": written,
+             "bytes": int(layout.stream_bytes) + written})
 
     def _restore_fused_dequant(self, restore, layer_payload, layout, kv_cache, block_ids, nb,
                                meta):
@@ -297,13 +370,15 @@ class OrigamiConnectorWorker:
             return None  # the blob must travel as plain bytes
         needed = -(-tokens // int(kv_cache.shape[2]))
         ids_dev = native_gpu.block_ids_tensor(block_ids[:needed], kv_cache.device, nb)
-        pipe = self._pipeline(kv_cache.device, layout.stream_bytes)
-        ids_dev.record_stream(pipe.compute_stream)
         quantizer = self.quantizer
-        event = pipe.submit(
-            self._fill_from_chunks(layer_payload, layout), layout.stream_bytes,
-            lambda flat: quantizer.dequantize_to_cache(flat, meta, kv_cache, ids_dev, tokens))
-        return _LayerLoadResult(event=event)
+        written = self._written_bytes(kv_cache, needed)
+        return self._submit_layer(
+            restore, layer_payload, layout, kv_cache, ids_dev,
+            lambda flat: quantizer.dequantize_to_cache(flat, meta, kv_cache, ids_dev, tokens),
+            "restore_materialize",
+            {"quantizer": quantizer.quantizer_id, "device": str(kv_cache.device),
+             "direct_to_kv_cache": True, "h2d_elided": False, "output_bytes": written,
+             "bytes": int(layout.stream_bytes) + written})
 
     def _restore_generic(self, restore, layer_payload, layout, kv_cache, block_ids):
         chunks = self.cpu_codec.decompress_many([r.compressed for r in layer_payload.chunks],
@@ -331,6 +406,62 @@ class OrigamiConnectorWorker:
             wait = not isinstance(result, _LayerLoadResult) or result.wait_on_current_stream
             if event is not None and wait and torch.cuda.is_available():
                 torch.cuda.current_stream().wait_event(event)
+            if isinstance(result, _LayerLoadResult):
+                self._flush_pending_cuda_metrics(result.pending_metrics)
+
+    def _flush_pending_cuda_metrics(self, pending_metrics: list | None,
+                                    final: bool = False) -> None:
+        """Writes event-timed metric rows (worker.py:574-617): ms from the
+        start/end events, and Gbit/s from input_bytes, output_bytes and bytes.
+        A row whose end event has not completed yet is kept and written by a
+        later call (the reference writes it at once, flagged
+        cuda_timing_deferred, and loses the time); with `final`, the events
+        are waited for."""
+        with self._metrics_lock:
+            rows = self._deferred_metrics + list(pending_metrics or [])
+            self._deferred_metrics = []
+        keep = []
+        for row in rows:
+            metric_type, restore, layer_payload, fields = row
+            start_event = fields.get("_cuda_start_event")
+            end_event = fields.get("_cuda_end_event")
+            if start_event is None or end_event is None:
+                self._write_restore_metric(metric_type, restore, layer_payload, fields)
+                continue
+            if final:
+                end_event.synchronize()
+            elif not end_event.query():
+                keep.append(row)
+                continue
+            out = {k: v for k, v in fields.items() if not k.startswith("_cuda_")}
+            ms = float(start_event.elapsed_time(end_event))
+            out["ms"] = ms
+            if metric_type == "h2d_copy":
+                out["h2d_ms"] = ms
+                out["h2d_gbps"] = int(out.get("bytes_copied", 0)) * 8.0 / ms / 1e6 if ms > 0 else 0.0
+                out["end_ts"] = time.time()
+                out["timing_complete"] = True
+            if ms > 0:
+                for key, name in (("input_bytes", "input_gbps"), ("output_bytes", "output_gbps"),
+                                  ("bytes", "gbps")):
+                    if int(out.get(key, 0) or 0):
+                        out[name] = int(out[key]) * 8.0 / ms / 1e6
+            self._write_restore_metric(metric_type, restore, layer_payload, out)
+        if keep:
+            with self._metrics_lock:
+                self._deferred_metrics = keep + self._deferred_metrics
+
+    def _write_restore_metric(self, metric_type: str, restore, layer_payload: LayerPayload,
+                              fields: dict[str, Any]) -> None:
+        """One JSONL row (worker.py:1751-1766)."""
+        if not self.metrics_path:
+            return
+        row = {"type": metric_type, "system": "origami",
+               "request_id": _restore_metric_id(restore),
+               "cache_key": restore.cache_key if restore is not None else "",
+               "layer_name": layer_payload.layer_name}
+        row.update(fields)
+        write_jsonl(self.metrics_path, row)
 
     # ------------------------------------------------------------------ save
 
@@ -463,6 +594,8 @@ class OrigamiConnectorWorker:
     # -------------------------------------------------------------- finished
 
     def get_finished(self) -> tuple[set[str], set[str]]:
+        self._flush_pending_cuda_metrics(None)
+        self._pipelines.prune()
         finished_recving: set[str] = set()
         for rf in list(self._restore_futures):
             if not rf.done():
@@ -490,5 +623,6 @@ class OrigamiConnectorWorker:
 
     def shutdown(self) -> None:
         self._executor.shutdown(wait=True)
-        for pipe in self._pipelines.values():
+        for pipe in self._pipelines.pipelines():
             pipe.synchronize()
+        self._flush_pending_cuda_metrics(None, final=True)
