@@ -1,0 +1,114 @@
+"""Full-size oracle parity at the benchmark geometries (one layer each):
+
+* Qwen2.5-7B batch: 4 KV heads, head_dim 128, bf16, block size 16; 8
+  requests with lengths default_rng(2).integers(8192, 65537, 8); each
+  request's first floor(T/2/16) blocks come from a prefix pool shared by all
+  block tables (in the source and in the destination cache);
+* Llama-3-8B fp8 e4m3: 8 KV heads, head_dim 128 (128-byte head rows), 16
+  requests of 16384 tokens, seed 3;
+* Llama-3-70B geometry: one 131072-token bf16 layer, 512 chunks of 1 MiB,
+  permuted block table, seed 4 (stream bit offsets pass 2**32).
+
+Chunks come from the planner at 1 MiB (chunking.py:22-123).  For every
+request the HIP pack from the paged cache must equal the oracle's pack of
+the gathered bytes, and the HIP restore into the destination cache must
+equal the oracle's unpack + scatter (benchmark_utils.py:350-444), over the
+whole cache, byte for byte."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from origami_amd.layout import kv_symbol_layout
+from origami_amd.lossless import native_gpu
+from origami_amd.lossless.chunking import plan_head_channel_chunks
+from origami_amd.synthetic import fill_layer
+
+pytestmark = pytest.mark.gpu
+
+BS = 16
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _oracle_threads():
+    oracle.set_threads(min(16, os.cpu_count() or 1))
+
+
+def _layout(T, H, C):
+    plan = plan_head_channel_chunks(layer_index=0, num_heads=H, head_dim=C, token_count=2 * T,
+                                    bytes_per_symbol=1, min_bytes=1 << 20,
+                                    target_bytes=1 << 20, max_bytes=1 << 20)
+    specs = [[c.layout.head_start, c.layout.head_end, c.layout.channel_start,
+              c.layout.channel_end, c.layout.token_start, c.layout.token_end] for c in plan]
+    return kv_symbol_layout(T, H, C, 8, specs)
+
+
+def _tables(perm, nblks, shared, pool):
+    cur, out = pool, []
+    for n, k in zip(nblks, shared):
+        out.append(np.concatenate([perm[:k], perm[cur:cur + n - k]]).astype(np.int64))
+        cur += n - k
+    return out
+
+
+def _run(dev, H, D, dtype, lengths, seed, shared_pool, expect_chunks=None):
+    esize = torch.empty((), dtype=dtype).element_size()
+    C = D * esize
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    nblks = [-(-int(T) // BS) for T in lengths]
+    shared = [int(T) // 2 // BS if shared_pool else 0 for T in lengths]
+    pool = max(shared) if shared_pool else 0
+    NB = pool + sum(n - k for n, k in zip(nblks, shared)) + 64
+    src = torch.zeros((2, NB, BS, H, D), dtype=dtype, device=dev)
+    fill_layer(src, torch.arange(NB, device=dev), gen)
+    src_tables = _tables(rng.permutation(NB), nblks, shared, pool)
+    dst_tables = _tables(rng.permutation(NB), nblks, shared, pool)
+    dst = torch.zeros_like(src)
+    src_u8 = src.view(torch.uint8).cpu().numpy()
+    expect = np.zeros_like(src_u8)
+    layouts = {}
+    for T, st, dt in zip(lengths, src_tables, dst_tables):
+        T = int(T)
+        lay = layouts.setdefault(T, _layout(T, H, C))
+        if expect_chunks is not None:
+            assert lay.num_chunks == expect_chunks
+        stream = native_gpu.pack_from_kv_cache(src, native_gpu.block_ids_tensor(st, dev, NB), T,
+                                               lay)
+        sym = oracle.gather_kv_cache(src_u8, st).reshape(2, -1, H, C)[:, :T].reshape(-1)
+        flat, offs = oracle.pack_canonical(sym, 8, lay.specs, [2 * T, H, C], [0, 1, 2, -1])
+        del sym
+        assert np.array_equal(stream.cpu().numpy(), flat), f"pack differs at T={T}"
+        native_gpu.unpack_to_kv_cache(stream, lay, T, dst,
+                                      native_gpu.block_ids_tensor(dt, dev, NB))
+        oracle.restore_layer(flat, offs, 8, lay.specs, T, H, C, dt, expect)
+        del flat, stream
+    got = dst.view(torch.uint8).cpu().numpy()
+    assert np.array_equal(got, expect), "restored cache differs from the oracle"
+    # and from the source blocks themselves (the prefix pool holds identical
+    # bytes for every request that references it)
+    for T, st, dt in zip(lengths, src_tables, dst_tables):
+        a = got[:, dt].reshape(2, -1, H, C)[:, :int(T)]
+        b = src_u8[:, st].reshape(2, -1, H, C)[:, :int(T)]
+        assert np.array_equal(a, b)
+    return NB, dst_tables
+
+
+def test_qwen25_7b_batch_full(cuda_device):
+    lengths = np.random.default_rng(2).integers(8192, 65537, 8)
+    assert not all(int(T) % 16 == 0 for T in lengths)  # ragged lengths are covered
+    NB, tables = _run(cuda_device, 4, 128, torch.bfloat16, lengths, 2, True)
+    # the destination prefix pool is referenced by every table
+    k = min(int(T) // 2 // BS for T in lengths)
+    assert all(np.array_equal(t[:k], tables[0][:k]) for t in tables)
+
+
+def test_llama3_8b_fp8_16x16k_full(cuda_device):
+    _run(cuda_device, 8, 128, torch.float8_e4m3fn, [16384] * 16, 3, False, expect_chunks=32)
+
+
+def test_llama3_70b_131072_full(cuda_device):
+    _run(cuda_device, 8, 128, torch.bfloat16, [131072], 4, False, expect_chunks=512)
