@@ -170,6 +170,27 @@ int origami_unpack_canonical_to_kv_cache(
     const int64_t* block_ids, int64_t block_count, origami_stream_t stream);
 
 /*
+ * Allocation-free variant of origami_unpack_canonical_to_kv_cache: same
+ * arguments, same results.  It has no counterpart in the reference.  It is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): it calls no
+ * hipMalloc, hipFree or other allocating routine and keeps no plan cache.
+ * A chunk plan in the planner's order needs no device metadata; the plane
+ * table of a reordered plan is written into a fixed 1 MiB device array per
+ * GPU (at most 131072 (head, channel) planes, i.e. num_heads * head_bytes;
+ * larger reordered plans return ORIGAMI_ERR_UNSUPPORTED).  That array is
+ * shared by every call on the GPU and keeps the last call's contents: calls
+ * that overlap on one GPU (different streams or threads) race.
+ */
+int origami_unpack_canonical_to_kv_cache_noalloc(
+    const uint8_t* flat_chunks, int64_t flat_bytes,
+    const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
+    const int64_t* chunk_specs, int64_t num_chunks, int64_t tokens,
+    void* kv_cache, int64_t cache_layout, int64_t num_blocks,
+    int64_t block_size, int64_t num_heads, int64_t head_bytes,
+    const int64_t* block_ids, int64_t block_count, origami_stream_t stream);
+
+/*
  * Fused save: gather a layer's K/V through the block table from the paged
  * cache and pack it into the canonical stream, in one pass; the inverse of
  * origami_unpack_canonical_to_kv_cache.  Replaces _select_blocks +

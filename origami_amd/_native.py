@@ -44,6 +44,8 @@ _SIGNATURES: dict[str, list] = {
         _p, _i64, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p],
     "origami_unpack_canonical_to_kv_cache": [
         _p, _i64, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "origami_unpack_canonical_to_kv_cache_noalloc": [
+        _p, _i64, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "origami_pack_canonical_from_kv_cache": [
         _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _i64, _p],
     "origami_scatter_kv_blocks": [_p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],

@@ -1164,6 +1164,197 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
 
 const int64_t kKvAxes[4] = {0, 1, 2, -1};
 
+// Checks shared by the fused restore entry points (sizes, cache geometry,
+// chunk metadata against the [2 * tokens, heads, head_bytes] symbol view).
+int check_fused_restore(const int64_t* offsets, const int64_t* bits, const int64_t* specs,
+                        int64_t n, int64_t flat_bytes, int64_t tokens, const void* kv_cache,
+                        int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+                        int64_t num_heads, int64_t head_bytes, int64_t block_count,
+                        int64_t* blk_stride, int64_t* half_stride) {
+  ORIGAMI_REQUIRE(tokens > 0 && num_heads > 0 && head_bytes > 0,
+                  "tokens, heads, and head_dim must be positive");
+  ORIGAMI_REQUIRE(block_size > 0, "kv_cache block size must be positive");
+  ORIGAMI_REQUIRE(num_blocks > 0, "kv_cache must hold at least one block");
+  ORIGAMI_REQUIRE(block_count > 0, "block_ids must be non-empty");
+  ORIGAMI_REQUIRE(tokens <= block_count * block_size, "tokens exceed destination block capacity");
+  const int64_t shape[3] = {2 * tokens, num_heads, head_bytes};
+  int rc = validate_layout(offsets, bits, specs, n, shape, 3, kKvAxes, 2 * tokens, num_heads,
+                           head_bytes, flat_bytes, nullptr);
+  if (rc) return rc;
+  rc = cache_geometry(cache_layout, num_blocks, block_size, blk_stride, half_stride);
+  if (rc) return rc;
+  if (head_bytes % 16 != 0 || !aligned16(kv_cache) || num_heads * head_bytes > kMaxPlaneTable)
+    return fail(ORIGAMI_ERR_UNSUPPORTED, "fused restore needs 16-byte head rows");
+  return ORIGAMI_OK;
+}
+
+// Row-kernel parameters of a fused restore (planes are set by the caller).
+RowsParams fused_restore_params(const uint8_t* flat, int64_t flat_bytes, int64_t tokens,
+                                void* kv_cache, int64_t num_blocks, int64_t block_size,
+                                int64_t num_heads, int64_t head_bytes, const int64_t* block_ids,
+                                int64_t block_count, int64_t blk_stride, int64_t half_stride) {
+  RowsParams p{};
+  set_stream(p, flat, flat_bytes);
+  p.rows = static_cast<uint8_t*>(kv_cache);
+  p.block_ids = block_ids;
+  p.num_blocks = num_blocks;
+  p.T = tokens;
+  p.row_tokens = block_count * block_size;
+  p.row_pitch = num_heads * head_bytes;
+  p.head_pitch = head_bytes;
+  p.bs = block_size;
+  p.blk_stride = blk_stride;
+  p.half_stride = half_stride;
+  return p;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free fused restore: the plane table of a reordered chunk plan
+// lives in `scratch`, a fixed device array, instead of library-allocated
+// memory, and the plan is analysed per call without the plan cache.
+// ---------------------------------------------------------------------------
+
+constexpr int64_t kScratchPlanes = 131072;  // int64 plane offsets: 1 MiB per GPU
+constexpr int kScratchDevices = 64;
+
+static __device__ __align__(256) int64_t scratch[kScratchPlanes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (each GPU holds its own copy of the array).  Host code must use this
+// address, never the array's name, which is only a host-side stand-in.
+int scratch_table(int64_t** out) {
+  static std::mutex mu;
+  static int64_t* ptrs[kScratchDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
+    return fail(ORIGAMI_ERR_HIP, "hipGetDevice failed (or device index above 63)");
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr)
+      return fail(ORIGAMI_ERR_HIP, std::string("hipGetSymbolAddress of the restore scratch "
+                                               "table failed: ") + hipGetErrorString(err));
+    ptrs[dev] = static_cast<int64_t*>(p);
+  }
+  *out = ptrs[dev];
+  return ORIGAMI_OK;
+}
+
+// The PlanInfo build_plane_table would give, from the chunk list alone: O(n),
+// plus an O(n^2) box-overlap test when the chunks are not in plane order.
+PlanInfo analyze_plan(const int64_t* offsets, const int64_t* bits, const int64_t* specs,
+                      int64_t n, int64_t T, int64_t H, int64_t C) {
+  PlanInfo info;
+  info.regular = n > 0;
+  info.bits = n > 0 ? static_cast<int>(bits[0]) : 0;
+  info.aligned16 = info.byte_aligned = info.planes_even = info.planes_dword = true;
+  bool in_order = true;  // chunk k holds planes [next, next + planes_k) in h * C + c order
+  int64_t next = 0;
+  for (int64_t k = 0; k < n; ++k) {
+    const int64_t* s = specs + 6 * k;
+    if (bits[k] != info.bits) info.bits = 0;
+    if (s[4] != 0 || s[5] != T) {
+      info.regular = false;
+      continue;
+    }
+    const int64_t planes = (s[1] - s[0]) * (s[3] - s[2]);
+    const int64_t first = offsets[k] * 8, step = T * bits[k];
+    auto all_multiple = [&](int64_t m) { return first % m == 0 && (planes == 1 || step % m == 0); };
+    if (!all_multiple(128)) info.aligned16 = false;
+    if (!all_multiple(8)) info.byte_aligned = false;
+    if (!all_multiple(16)) info.planes_even = false;
+    if (!all_multiple(32)) info.planes_dword = false;
+    if (in_order) {
+      const bool one_run = s[1] - s[0] == 1 || (s[2] == 0 && s[3] == C);
+      in_order = one_run && s[0] * C + s[2] == next && first == offsets[0] * 8 + next * step;
+      next += planes;
+    }
+  }
+  if (info.regular && !in_order) {
+    // reordered boxes: a plane covered twice makes the plan irregular
+    for (int64_t a = 0; a < n && info.regular; ++a) {
+      const int64_t* sa = specs + 6 * a;
+      for (int64_t b = a + 1; b < n; ++b) {
+        const int64_t* sb = specs + 6 * b;
+        if (sa[0] < sb[1] && sb[0] < sa[1] && sa[2] < sb[3] && sb[2] < sa[3]) {
+          info.regular = false;
+          break;
+        }
+      }
+    }
+  }
+  if (info.bits != 8) info.aligned16 = false;
+  if (!info.regular) {
+    info.aligned16 = info.byte_aligned = info.planes_even = info.planes_dword = false;
+  }
+  if (info.regular && info.bits != 0 && in_order && next == H * C && H * C > 0) {
+    info.dense = true;
+    info.dense_base = offsets[0] * 8;
+  }
+  return info;
+}
+
+constexpr int kFillChunks = 32;  // chunk boxes per table-fill launch (kernel arguments)
+
+struct PlaneFill {
+  int64_t C;           // channels per head
+  int64_t plane_bits;  // T * b: bits per plane
+  int32_t n;           // chunks in this launch
+  int64_t first_bit[kFillChunks];  // bit offset of each chunk's first symbol
+  int32_t box[kFillChunks][4];     // head_start, head_end, channel_start, channel_end
+};
+
+__global__ __launch_bounds__(kThreads) void fill_i64_kernel(int64_t* __restrict__ p, int64_t n,
+                                                            int64_t value) {
+  const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step)
+    p[i] = value;
+}
+
+// table[h * C + c] = bit offset of plane (h, c) for the chunks of one launch
+// (local plane order head-major, then channel: bitpack_layout_cuda.cu:110-124).
+__global__ __launch_bounds__(kThreads) void plane_table_kernel(PlaneFill f,
+                                                               int64_t* __restrict__ table) {
+  const int j = static_cast<int>(blockIdx.y);
+  if (j >= f.n) return;
+  const int64_t hs = f.box[j][0], cs = f.box[j][2];
+  const int64_t cc = f.box[j][3] - cs;
+  const int64_t planes = (f.box[j][1] - hs) * cc;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < planes;
+       i += step) {
+    const int64_t h = hs + i / cc, c = cs + i % cc;
+    table[h * f.C + c] = f.first_bit[j] + i * f.plane_bits;
+  }
+}
+
+// Writes the plane table of a regular, uniform-width plan into `table`
+// (H * C entries, -1 for planes no chunk covers), on `stream`.
+int fill_plane_table(int64_t* table, const int64_t* offsets, const int64_t* specs, int64_t n,
+                     int64_t T, int64_t H, int64_t C, int bits, hipStream_t stream) {
+  hipLaunchKernelGGL(fill_i64_kernel, dim3(grid_for(H * C, kThreads, 1024)), dim3(kThreads), 0,
+                     stream, table, H * C, int64_t(-1));
+  if (int rc = check_launch("fill_i64_kernel")) return rc;
+  for (int64_t k0 = 0; k0 < n; k0 += kFillChunks) {
+    PlaneFill f{};
+    f.C = C;
+    f.plane_bits = T * bits;
+    f.n = static_cast<int32_t>(std::min<int64_t>(kFillChunks, n - k0));
+    int64_t most = 0;
+    for (int j = 0; j < f.n; ++j) {
+      const int64_t* s = specs + 6 * (k0 + j);
+      f.first_bit[j] = offsets[k0 + j] * 8;
+      for (int a = 0; a < 4; ++a) f.box[j][a] = static_cast<int32_t>(s[a]);
+      most = std::max(most, (s[1] - s[0]) * (s[3] - s[2]));
+    }
+    hipLaunchKernelGGL(plane_table_kernel, dim3(grid_for(most, kThreads, 1024), f.n),
+                       dim3(kThreads), 0, stream, f, table);
+    if (int rc = check_launch("plane_table_kernel")) return rc;
+  }
+  return ORIGAMI_OK;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -1327,22 +1518,11 @@ int origami_unpack_canonical_to_kv_cache(
     int64_t num_heads, int64_t head_bytes, const int64_t* block_ids, int64_t block_count,
     origami_stream_t stream_) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  ORIGAMI_REQUIRE(tokens > 0 && num_heads > 0 && head_bytes > 0,
-                  "tokens, heads, and head_dim must be positive");
-  ORIGAMI_REQUIRE(block_size > 0, "kv_cache block size must be positive");
-  ORIGAMI_REQUIRE(num_blocks > 0, "kv_cache must hold at least one block");
-  ORIGAMI_REQUIRE(block_count > 0, "block_ids must be non-empty");
-  ORIGAMI_REQUIRE(tokens <= block_count * block_size, "tokens exceed destination block capacity");
-  const int64_t shape[3] = {2 * tokens, num_heads, head_bytes};
-  int rc = validate_layout(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, shape, 3,
-                           kKvAxes, 2 * tokens, num_heads, head_bytes, flat_bytes, nullptr);
-  if (rc) return rc;
   int64_t blk_stride = 0, half_stride = 0;
-  rc = cache_geometry(cache_layout, num_blocks, block_size, &blk_stride, &half_stride);
+  int rc = check_fused_restore(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, flat_bytes,
+                               tokens, kv_cache, cache_layout, num_blocks, block_size, num_heads,
+                               head_bytes, block_count, &blk_stride, &half_stride);
   if (rc) return rc;
-  if (head_bytes % 16 != 0 || !aligned16(kv_cache) ||
-      num_heads * head_bytes > kMaxPlaneTable)
-    return fail(ORIGAMI_ERR_UNSUPPORTED, "fused restore needs 16-byte head rows");
   std::shared_ptr<const Plan> plan;
   rc = get_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, 2 * tokens, num_heads,
                 head_bytes, true, &plan);
@@ -1350,22 +1530,53 @@ int origami_unpack_canonical_to_kv_cache(
   if (!plan->has_table || !plan->info.regular || plan->info.bits == 0)
     return fail(ORIGAMI_ERR_UNSUPPORTED,
                 "fused restore needs chunks spanning all tokens with one bit width");
-  RowsParams p{};
-  set_stream(p, flat_chunks, flat_bytes);
+  RowsParams p = fused_restore_params(flat_chunks, flat_bytes, tokens, kv_cache, num_blocks,
+                                      block_size, num_heads, head_bytes, block_ids, block_count,
+                                      blk_stride, half_stride);
   if (int rc2 = set_planes(p, plan)) return rc2;
-  p.rows = static_cast<uint8_t*>(kv_cache);
-  p.block_ids = block_ids;
-  p.num_blocks = num_blocks;
-  p.T = tokens;
-  p.row_tokens = block_count * block_size;
-  p.row_pitch = num_heads * head_bytes;
-  p.head_pitch = head_bytes;
-  p.bs = block_size;
-  p.blk_stride = blk_stride;
-  p.half_stride = half_stride;
   set_grid_dims(p, num_heads, head_bytes, p.row_tokens, 2);
   return launch_rows(false, p, 2, plan->info.bits, rows_mode(plan->info, p, tokens, false),
                      stream);
+}
+
+int origami_unpack_canonical_to_kv_cache_noalloc(
+    const uint8_t* flat_chunks, int64_t flat_bytes, const int64_t* chunk_offsets,
+    const int64_t* bits_per_chunk, const int64_t* chunk_specs, int64_t num_chunks, int64_t tokens,
+    void* kv_cache, int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+    int64_t num_heads, int64_t head_bytes, const int64_t* block_ids, int64_t block_count,
+    origami_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  int64_t blk_stride = 0, half_stride = 0;
+  int rc = check_fused_restore(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, flat_bytes,
+                               tokens, kv_cache, cache_layout, num_blocks, block_size, num_heads,
+                               head_bytes, block_count, &blk_stride, &half_stride);
+  if (rc) return rc;
+  const PlanInfo info = analyze_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks,
+                                     2 * tokens, num_heads, head_bytes);
+  if (!info.regular || info.bits == 0)
+    return fail(ORIGAMI_ERR_UNSUPPORTED,
+                "fused restore needs chunks spanning all tokens with one bit width");
+  RowsParams p = fused_restore_params(flat_chunks, flat_bytes, tokens, kv_cache, num_blocks,
+                                      block_size, num_heads, head_bytes, block_ids, block_count,
+                                      blk_stride, half_stride);
+  if (info.dense) {
+    p.planes = nullptr;
+    p.plane_base = info.dense_base;
+    p.plane_bits = 2 * tokens * info.bits;
+  } else {
+    if (num_heads * head_bytes > kScratchPlanes)
+      return fail(ORIGAMI_ERR_UNSUPPORTED,
+                  "allocation-free restore of a reordered chunk plan supports at most 131072 "
+                  "(head, channel) planes (num_heads * head_bytes)");
+    int64_t* table = nullptr;
+    if (int rc2 = scratch_table(&table)) return rc2;
+    if (int rc2 = fill_plane_table(table, chunk_offsets, chunk_specs, num_chunks, 2 * tokens,
+                                   num_heads, head_bytes, info.bits, stream))
+      return rc2;
+    p.planes = table;
+  }
+  set_grid_dims(p, num_heads, head_bytes, p.row_tokens, 2);
+  return launch_rows(false, p, 2, info.bits, rows_mode(info, p, tokens, false), stream);
 }
 
 int origami_pack_canonical_from_kv_cache(

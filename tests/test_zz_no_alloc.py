@@ -1,0 +1,105 @@
+"""Allocation-free fused restore: origami_unpack_canonical_to_kv_cache_noalloc,
+called through the C ABI, gives byte for byte what
+origami_unpack_canonical_to_kv_cache gives, on two calls in a row (the
+second with a smaller layer), for chunk plans in the planner's order (no
+device metadata) and reordered ones (plane table in the fixed scratch
+array, rewritten by every call), and rejects a reordered plan above the
+scratch maximum."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from origami_amd import _native
+from origami_amd.layout import kv_symbol_layout
+from origami_amd.lossless import native_gpu
+from origami_amd.lossless.chunking import plan_head_channel_chunks
+
+pytestmark = pytest.mark.gpu
+
+FUSED = "origami_unpack_canonical_to_kv_cache"
+NOALLOC = "origami_unpack_canonical_to_kv_cache_noalloc"
+
+
+def _planner_specs(T2, H, C, target):
+    return [[c.layout.head_start, c.layout.head_end, c.layout.channel_start,
+             c.layout.channel_end, 0, T2]
+            for c in plan_head_channel_chunks(layer_index=0, num_heads=H, head_dim=C,
+                                              token_count=T2, bytes_per_symbol=1,
+                                              min_bytes=target, target_bytes=target,
+                                              max_bytes=target)]
+
+
+def _specs(kind, T, H, C, rng):
+    specs = _planner_specs(2 * T, H, C, 1 << 14)
+    if kind == "planner":
+        return specs
+    order = rng.permutation(len(specs))
+    specs = [specs[i] for i in order]
+    if kind == "reordered_partial":
+        specs = specs[: max(1, len(specs) * 2 // 3)]  # some planes uncovered -> zeros
+    return specs
+
+
+def _restore(name, flat, lay, T, cache, ids):
+    code, nb, bs, H, C = native_gpu.cache_geometry(cache)
+    _native.call(name, flat.data_ptr(), flat.numel(), *lay.native_args, int(T),
+                 cache.data_ptr(), code, nb, bs, H, C, ids.data_ptr(), ids.numel(),
+                 native_gpu._stream_handle(cache.device))
+
+
+def _case(dev, rng, kind, T, H, C, bits, bs, blocks_first):
+    nblk = -(-T // bs)
+    NB = nblk + 11
+    specs = _specs(kind, T, H, C, rng)
+    lay = kv_symbol_layout(T, H, C, bits, specs)
+    sym = rng.integers(0, 256, 2 * T * H * C, dtype=np.uint8)
+    flat_np, offs = oracle.pack_canonical(sym, bits, specs, [2 * T, H, C], [0, 1, 2, -1])
+    flat = torch.from_numpy(flat_np).to(dev)
+    ids_np = rng.permutation(NB)[:nblk].astype(np.int64)
+    ids = torch.from_numpy(ids_np).to(dev)
+    shape = (NB, 2, bs, H, C) if blocks_first else (2, NB, bs, H, C)
+    caches = {name: torch.full(shape, 0x5A, dtype=torch.uint8, device=dev)
+              for name in (FUSED, NOALLOC)}
+    for name, cache in caches.items():
+        _restore(name, flat, lay, T, cache, ids)
+    torch.cuda.synchronize(dev)
+    got = caches[NOALLOC].cpu().numpy()
+    assert np.array_equal(got, caches[FUSED].cpu().numpy()), (kind, T, H, C, bits)
+    expect = np.full(shape, 0x5A, dtype=np.uint8)
+    oracle.restore_layer(flat_np, offs, bits, specs, T, H, C, ids_np, expect,
+                         blocks_first=blocks_first)
+    assert np.array_equal(got, expect), (kind, T, H, C, bits)
+
+
+@pytest.mark.parametrize("kind", ["planner", "reordered", "reordered_partial"])
+@pytest.mark.parametrize("bits", [8, 5])
+def test_noalloc_matches_fused_restore_twice(cuda_device, kind, bits):
+    rng = np.random.default_rng(100 + bits)
+    # first call, then a smaller layer (fewer tokens, heads and channels)
+    _case(cuda_device, rng, kind, 1000, 8, 256, bits, 16, False)
+    _case(cuda_device, rng, kind, 300, 4, 128, bits, 16, True)
+
+
+def test_noalloc_alternating_plans_rewrite_scratch(cuda_device):
+    """A reordered plan, then a partial one of the same geometry: planes the
+    second plan leaves uncovered must read as uncovered, not as the first
+    call's offsets still in the scratch array."""
+    rng = np.random.default_rng(7)
+    for kind in ("reordered", "reordered_partial", "reordered", "planner"):
+        _case(cuda_device, rng, kind, 640, 4, 256, 8, 16, False)
+
+
+def test_noalloc_rejects_reordered_plan_above_scratch_maximum(cuda_device):
+    T, H, C, bs = 16, 1024, 256, 16  # 262144 planes > 131072
+    specs = [[H // 2, H, 0, C, 0, 2 * T], [0, H // 2, 0, C, 0, 2 * T]]
+    lay = kv_symbol_layout(T, H, C, 8, specs)
+    flat = torch.zeros(lay.stream_bytes, dtype=torch.uint8, device=cuda_device)
+    cache = torch.zeros((2, 2, bs, H, C), dtype=torch.uint8, device=cuda_device)
+    ids = torch.tensor([1], dtype=torch.int64, device=cuda_device)
+    with pytest.raises(_native.OrigamiNativeError, match="at most 131072") as err:
+        _restore(NOALLOC, flat, lay, T, cache, ids)
+    assert err.value.code == _native.ORIGAMI_ERR_UNSUPPORTED
+    # the allocating entry point serves it (its plane table is allocated)
+    _restore(FUSED, flat, lay, T, cache, ids)
+    torch.cuda.synchronize(cuda_device)
