@@ -56,6 +56,9 @@ typedef struct ihipStream_t* origami_stream_t; /* == hipStream_t */
 #define ORIGAMI_CACHE_KV_FIRST 0
 #define ORIGAMI_CACHE_BLOCKS_FIRST 1
 
+/* origami_unpack_canonical_to_kv_cache_batch flags */
+#define ORIGAMI_BATCH_SKIP_UNWRITTEN 1 /* read nothing for destination blocks that are skipped */
+
 /* element types of dequantize inputs and outputs */
 #define ORIGAMI_DTYPE_FLOAT16 1
 #define ORIGAMI_DTYPE_BFLOAT16 2
@@ -189,6 +192,32 @@ int origami_unpack_canonical_to_kv_cache_noalloc(
     void* kv_cache, int64_t cache_layout, int64_t num_blocks,
     int64_t block_size, int64_t num_heads, int64_t head_bytes,
     const int64_t* block_ids, int64_t block_count, origami_stream_t stream);
+
+/*
+ * Batched fused restore: one layer of several requests into one paged cache.
+ * Request r is exactly the argument set of origami_unpack_canonical_to_kv_cache
+ * (stream flat_chunks[r] of flat_bytes[r] bytes, its chunk metadata arrays,
+ * tokens[r], device block table block_ids[r] of block_counts[r] ids); the
+ * cache geometry is shared.  Requests whose plans share a symbol width and
+ * addressing mode go to one launch (up to 16 per launch), so a batch of short
+ * requests fills the GPU like one long one.  Replaces the per-request loop of
+ * the reference's layer restore (worker.py:796-897 and 1087-1248, one
+ * unpack + copy_kv_to_hbm per request and layer).  The requests of one call
+ * run concurrently: two requests must not carry different bytes for the same
+ * destination block (vLLM's shared prefix blocks hold the same bytes).  Block
+ * ids outside [0, num_blocks) are skipped, as in the single restore; with
+ * ORIGAMI_BATCH_SKIP_UNWRITTEN (block_size a multiple of 16) the stream bytes
+ * of a skipped block are not read either, so a caller can write a shared
+ * prefix block once by passing -1 for its later occurrences.  All requests
+ * are validated before anything is launched.
+ */
+int origami_unpack_canonical_to_kv_cache_batch(
+    int64_t num_requests, const uint8_t* const* flat_chunks, const int64_t* flat_bytes,
+    const int64_t* const* chunk_offsets, const int64_t* const* bits_per_chunk,
+    const int64_t* const* chunk_specs, const int64_t* num_chunks, const int64_t* tokens,
+    void* kv_cache, int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+    int64_t num_heads, int64_t head_bytes, const int64_t* const* block_ids,
+    const int64_t* block_counts, int64_t flags, origami_stream_t stream);
 
 /*
  * Fused save: gather a layer's K/V through the block table from the paged

@@ -447,6 +447,30 @@ struct RowsParams {
   int32_t nqt;               // workgroups along channels
   int32_t nst;               // workgroups along tokens
   int64_t ntiles;            // workgroup tiles; a workgroup loops over tiles
+  int32_t skip_dead;         // unpack: a lane whose destination block id is outside
+                             // [0, num_blocks) reads nothing (bs a multiple of 16)
+};
+
+// Per-request fields of a batched restore (one layer of several requests
+// into one cache, one launch); the rest of RowsParams is shared.
+struct RowsRequest {
+  uint8_t* stream;
+  int64_t stream_bytes, bit_bias;
+  const int64_t* planes;
+  int64_t plane_base, plane_bits;
+  const int64_t* block_ids;
+  int64_t T, row_tokens;
+  int64_t tile0;  // first workgroup tile of the request
+  int32_t nst;
+  int32_t skip_dead;
+};
+
+constexpr int kBatchRequests = 16;  // requests per batched launch (kernel arguments)
+
+struct RowsBatch {
+  RowsParams common;
+  int32_t nreq;
+  RowsRequest req[kBatchRequests];
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -764,8 +788,14 @@ __device__ __forceinline__ void unpack_tile(const RowsParams& p, int64_t tile,
                                             const int64_t* desc) {
   const TileCoord tc = tile_coord(p, tile);
   if (tc.q >= p.nq || tc.t0 >= p.row_tokens) return;
-  const int64_t nv = p.T - tc.t0;  // tokens of this segment that hold symbols
+  int64_t nv = p.T - tc.t0;  // tokens of this segment that hold symbols
   const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
+  if (p.skip_dead) {
+    // the lane's 16 tokens lie in one block (bs % 16 == 0): an id outside the
+    // cache means nothing of the segment is written, so nothing is read
+    const int64_t pid = p.block_ids[tc.t0 / p.bs];
+    if (pid < 0 || pid >= p.num_blocks) nv = 0;
+  }
 
   uint32_t v[16][4];
 #pragma unroll
@@ -815,6 +845,33 @@ __global__ __launch_bounds__(kRowsThreads) void rows_unpack_kernel(RowsParams p)
   for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     load_descriptors(p, tile, desc);
     unpack_tile<BITS, MODE>(p, tile, desc);
+  }
+}
+
+// One layer of several requests: the workgroup's tile range picks the
+// request (a uniform scan of at most kBatchRequests tile offsets).
+template <int BITS, int MODE>
+__global__ __launch_bounds__(kRowsThreads) void rows_unpack_batch_kernel(RowsBatch b) {
+  __shared__ int64_t desc[kTilePlanes];
+  for (int64_t tile = blockIdx.x; tile < b.common.ntiles; tile += gridDim.x) {
+    int r = 0;
+    while (r + 1 < b.nreq && tile >= b.req[r + 1].tile0) ++r;
+    const RowsRequest& q = b.req[r];
+    RowsParams p = b.common;
+    p.stream = q.stream;
+    p.stream_bytes = q.stream_bytes;
+    p.bit_bias = q.bit_bias;
+    p.planes = q.planes;
+    p.plane_base = q.plane_base;
+    p.plane_bits = q.plane_bits;
+    p.block_ids = q.block_ids;
+    p.T = q.T;
+    p.row_tokens = q.row_tokens;
+    p.nst = q.nst;
+    p.skip_dead = q.skip_dead;
+    const int64_t local = tile - q.tile0;
+    load_descriptors(p, local, desc);
+    unpack_tile<BITS, MODE>(p, local, desc);
   }
 }
 
@@ -1100,6 +1157,80 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
     const int64_t tiles = nhalf * H * static_cast<int64_t>(p.nqt) * p.nst;
     if (tiles >= want || waves == 4) break;
   }
+}
+
+// Workgroup shape of a batched restore: set_grid_dims' rule with the launch
+// size summed over the requests (each request has its own token tiles), then
+// each request's tile count and first tile.
+void set_batch_grid(RowsBatch& b, int64_t H, int64_t C) {
+  RowsParams& p = b.common;
+  if (H > 1 && p.head_pitch == C) {
+    C *= H;
+    H = 1;
+  }
+  p.H = static_cast<int32_t>(H);
+  p.C = C;
+  p.nq = static_cast<int32_t>(C / 16);
+  const int nqg = (p.nq + kLaneGroups - 1) / kLaneGroups;
+  const int64_t want = 2 * static_cast<int64_t>(device_cu_count());
+  auto nst_of = [&](int64_t row_tokens) {
+    const int64_t segs = (row_tokens + kSegTokens - 1) / kSegTokens;
+    const int64_t segs_per_wg = static_cast<int64_t>(p.ws) * kLaneSegs;
+    return (segs + segs_per_wg - 1) / segs_per_wg;
+  };
+  for (int waves = kRowsMaxWaves;; waves /= 2) {
+    const int wq_cap = waves == kRowsMaxWaves ? kRowsWq : 2;
+    int wq = 1;
+    while (wq < wq_cap && wq * 2 <= nqg) wq *= 2;
+    p.waves = waves;
+    p.wq = wq;
+    p.ws = waves / wq;
+    p.nqt = (nqg + wq - 1) / wq;
+    int64_t tiles = 0;
+    for (int r = 0; r < b.nreq; ++r) tiles += 2 * H * p.nqt * nst_of(b.req[r].row_tokens);
+    if (tiles >= want || waves == 4) break;
+  }
+  int64_t tile0 = 0;
+  for (int r = 0; r < b.nreq; ++r) {
+    b.req[r].nst = static_cast<int32_t>(nst_of(b.req[r].row_tokens));
+    b.req[r].tile0 = tile0;
+    tile0 += 2 * H * p.nqt * static_cast<int64_t>(b.req[r].nst);
+  }
+  p.ntiles = tile0;
+}
+
+int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream) {
+  if (b.common.ntiles <= 0) return ORIGAMI_OK;
+  int64_t blocks = b.common.ntiles;
+  if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
+  if (blocks > INT32_MAX) blocks = INT32_MAX;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(64 * b.common.waves));
+  if (bits == 8 && mode == kRowsAligned16) {
+    hipLaunchKernelGGL((rows_unpack_batch_kernel<8, kRowsAligned16>), grid, block, 0, stream, b);
+    return check_launch("rows_unpack_batch_kernel");
+  }
+  const bool window = mode == kRowsWindow;
+#define ORIGAMI_BATCH_CASE(B)                                                                    \
+  case B:                                                                                        \
+    if (window)                                                                                  \
+      hipLaunchKernelGGL((rows_unpack_batch_kernel<B, kRowsWindow>), grid, block, 0, stream, b); \
+    else                                                                                         \
+      hipLaunchKernelGGL((rows_unpack_batch_kernel<B, kRowsShift>), grid, block, 0, stream, b);  \
+    break;
+  switch (bits) {
+    ORIGAMI_BATCH_CASE(1)
+    ORIGAMI_BATCH_CASE(2)
+    ORIGAMI_BATCH_CASE(3)
+    ORIGAMI_BATCH_CASE(4)
+    ORIGAMI_BATCH_CASE(5)
+    ORIGAMI_BATCH_CASE(6)
+    ORIGAMI_BATCH_CASE(7)
+    ORIGAMI_BATCH_CASE(8)
+    default:
+      return fail(ORIGAMI_ERR_INVALID, "Origami CUDA bitpack supports only 1..8 bit symbols");
+  }
+#undef ORIGAMI_BATCH_CASE
+  return check_launch("rows_unpack_batch_kernel");
 }
 
 // Addressing mode of the row kernels for this plan and stream: `T` is the
@@ -1577,6 +1708,78 @@ int origami_unpack_canonical_to_kv_cache_noalloc(
   }
   set_grid_dims(p, num_heads, head_bytes, p.row_tokens, 2);
   return launch_rows(false, p, 2, info.bits, rows_mode(info, p, tokens, false), stream);
+}
+
+int origami_unpack_canonical_to_kv_cache_batch(
+    int64_t num_requests, const uint8_t* const* flat_chunks, const int64_t* flat_bytes,
+    const int64_t* const* chunk_offsets, const int64_t* const* bits_per_chunk,
+    const int64_t* const* chunk_specs, const int64_t* num_chunks, const int64_t* tokens,
+    void* kv_cache, int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+    int64_t num_heads, int64_t head_bytes, const int64_t* const* block_ids,
+    const int64_t* block_counts, int64_t flags, origami_stream_t stream_) {
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  ORIGAMI_REQUIRE(num_requests >= 0, "request count must be non-negative");
+  ORIGAMI_REQUIRE((flags & ~int64_t(ORIGAMI_BATCH_SKIP_UNWRITTEN)) == 0, "unknown batch flags");
+  const bool skip = (flags & ORIGAMI_BATCH_SKIP_UNWRITTEN) != 0;
+  ORIGAMI_REQUIRE(!skip || block_size % 16 == 0,
+                  "skipping unwritten blocks needs a block size that is a multiple of 16");
+  // validate and plan every request before anything is launched
+  struct Item {
+    RowsRequest q;
+    int bits, mode;
+  };
+  std::vector<Item> items;
+  items.reserve(static_cast<size_t>(num_requests));
+  RowsParams common{};
+  for (int64_t r = 0; r < num_requests; ++r) {
+    int64_t blk_stride = 0, half_stride = 0;
+    int rc = check_fused_restore(chunk_offsets[r], bits_per_chunk[r], chunk_specs[r],
+                                 num_chunks[r], flat_bytes[r], tokens[r], kv_cache, cache_layout,
+                                 num_blocks, block_size, num_heads, head_bytes, block_counts[r],
+                                 &blk_stride, &half_stride);
+    if (rc) return rc;
+    std::shared_ptr<const Plan> plan;
+    rc = get_plan(chunk_offsets[r], bits_per_chunk[r], chunk_specs[r], num_chunks[r],
+                  2 * tokens[r], num_heads, head_bytes, true, &plan);
+    if (rc) return rc;
+    if (!plan->has_table || !plan->info.regular || plan->info.bits == 0)
+      return fail(ORIGAMI_ERR_UNSUPPORTED,
+                  "fused restore needs chunks spanning all tokens with one bit width");
+    RowsParams p = fused_restore_params(flat_chunks[r], flat_bytes[r], tokens[r], kv_cache,
+                                        num_blocks, block_size, num_heads, head_bytes,
+                                        block_ids[r], block_counts[r], blk_stride, half_stride);
+    if (int rc2 = set_planes(p, plan)) return rc2;
+    if (r == 0) common = p;
+    Item it{};
+    it.q.stream = p.stream;
+    it.q.stream_bytes = p.stream_bytes;
+    it.q.bit_bias = p.bit_bias;
+    it.q.planes = p.planes;
+    it.q.plane_base = p.plane_base;
+    it.q.plane_bits = p.plane_bits;
+    it.q.block_ids = p.block_ids;
+    it.q.T = p.T;
+    it.q.row_tokens = p.row_tokens;
+    it.q.skip_dead = skip ? 1 : 0;
+    it.bits = plan->info.bits;
+    it.mode = rows_mode(plan->info, p, tokens[r], false);
+    items.push_back(it);
+  }
+  // one launch per (width, addressing mode) group of up to kBatchRequests
+  std::vector<bool> done(items.size(), false);
+  for (size_t i = 0; i < items.size(); ++i) {
+    if (done[i]) continue;
+    RowsBatch b{};
+    b.common = common;
+    for (size_t j = i; j < items.size() && b.nreq < kBatchRequests; ++j) {
+      if (done[j] || items[j].bits != items[i].bits || items[j].mode != items[i].mode) continue;
+      b.req[b.nreq++] = items[j].q;
+      done[j] = true;
+    }
+    set_batch_grid(b, num_heads, head_bytes);
+    if (int rc = launch_rows_batch(b, items[i].bits, items[i].mode, stream)) return rc;
+  }
+  return ORIGAMI_OK;
 }
 
 int origami_pack_canonical_from_kv_cache(

@@ -308,6 +308,106 @@ def _tokens_major_to_layout(value: torch.Tensor, layout: CanonicalLayout) -> tor
     return out.reshape(-1)
 
 
+def batch_block_tables(block_tables: Sequence, tokens: Sequence[int], block_size: int,
+                       dedup: bool) -> tuple[list[np.ndarray], bool]:
+    """Host block tables of a batched restore, and whether the requests may
+    share one launch.  A destination block that several requests restore as a
+    full block (all block_size tokens valid) holds the same bytes in each
+    (vLLM shares only full prefix blocks); with `dedup` its later occurrences
+    become -1, so it is read and written once.  A block that is partial in any
+    request that shares it would receive different bytes, so such a batch
+    must run request by request (returned flag False)."""
+    tables = [np.ascontiguousarray(np.asarray(t, dtype=np.int64).reshape(-1))
+              for t in block_tables]
+    if len(tables) < 2:
+        return tables, True
+    full = [np.arange(1, t.size + 1) * block_size <= int(T) for t, T in zip(tables, tokens)]
+    cat = np.concatenate(tables)
+    fcat = np.concatenate(full)
+    uniq, first = np.unique(cat, return_index=True)
+    first_of = first[np.searchsorted(uniq, cat)]
+    dup = np.arange(cat.size) != first_of
+    if not dup.any():
+        return tables, True
+    if (dup & ~(fcat & fcat[first_of])).any():
+        return tables, False
+    if dedup:
+        cat = cat.copy()
+        cat[dup] = -1
+        bounds = np.cumsum([0] + [t.size for t in tables])
+        tables = [cat[bounds[i]:bounds[i + 1]] for i in range(len(tables))]
+    return tables, True
+
+
+def unpack_batch_to_kv_cache(requests: Sequence[tuple], kv_cache: torch.Tensor, *,
+                             dedup_shared_blocks: bool = False) -> None:
+    """Fused restore of one layer of several requests into one cache, in one
+    launch per symbol width and addressing mode (the reference restores
+    request by request, worker.py:796-897 and 1087-1248).  `requests` holds
+    (flat stream, kv_symbol_layout, tokens, block ids) per request, block ids
+    as a host sequence.  The result equals restoring the requests one after
+    another; with `dedup_shared_blocks` a full block shared by several requests
+    is read and written once."""
+    _require_cuda(kv_cache, "kv_cache")
+    code, nb, bs, H, head_bytes = cache_geometry(kv_cache)
+    reqs = list(requests)
+    if not reqs:
+        return
+    for flat, layout, tokens, _ in reqs:
+        _require_cuda(flat, "flat_chunks")
+        if (layout.token_count != 2 * int(tokens) or layout.num_heads != H
+                or layout.head_dim != head_bytes):
+            raise RuntimeError("symbol layout does not match the kv_cache geometry")
+    host_tables = []
+    for _, _, tokens, ids in reqs:
+        ids_np = (ids.detach().to("cpu", torch.int64).numpy() if isinstance(ids, torch.Tensor)
+                  else np.asarray(ids, dtype=np.int64))
+        if ids_np.size == 0:
+            raise RuntimeError("block_ids must be non-empty")
+        if int(ids_np.min()) < 0 or int(ids_np.max()) >= nb:
+            raise RuntimeError("block id out of range for kv_cache")
+        host_tables.append(ids_np)
+    tables, batchable = batch_block_tables(host_tables, [int(r[2]) for r in reqs], bs,
+                                           dedup_shared_blocks and bs % 16 == 0)
+    device = kv_cache.device
+    if not batchable:
+        for (flat, layout, tokens, _), t in zip(reqs, tables):
+            unpack_to_kv_cache(flat, layout, int(tokens), kv_cache,
+                               torch.from_numpy(t).to(device))
+        return
+    dev_tables = torch.from_numpy(np.concatenate(tables)).to(device)
+    bounds = np.cumsum([0] + [t.size for t in tables])
+    n = len(reqs)
+    ptr = lambda vals: np.ascontiguousarray(np.asarray(vals, dtype=np.uint64))  # noqa: E731
+    i64 = lambda vals: np.ascontiguousarray(np.asarray(vals, dtype=np.int64))  # noqa: E731
+    flats = ptr([r[0].data_ptr() for r in reqs])
+    flat_bytes = i64([r[0].numel() for r in reqs])
+    offs = ptr([r[1].offsets.ctypes.data for r in reqs])
+    bits = ptr([r[1].bits.ctypes.data for r in reqs])
+    specs = ptr([r[1].specs.ctypes.data for r in reqs])
+    nchunks = i64([r[1].num_chunks for r in reqs])
+    toks = i64([int(r[2]) for r in reqs])
+    base = dev_tables.data_ptr()
+    ids_ptrs = ptr([base + 8 * int(bounds[i]) for i in range(n)])
+    counts = i64([t.size for t in tables])
+    flags = _native.BATCH_SKIP_UNWRITTEN if dedup_shared_blocks and bs % 16 == 0 else 0
+    with _device_guard(device):
+        try:
+            _native.call(
+                "origami_unpack_canonical_to_kv_cache_batch", n, flats.ctypes.data,
+                flat_bytes.ctypes.data, offs.ctypes.data, bits.ctypes.data, specs.ctypes.data,
+                nchunks.ctypes.data, toks.ctypes.data, kv_cache.data_ptr(), code, nb, bs, H,
+                head_bytes, ids_ptrs.ctypes.data, counts.ctypes.data, flags,
+                _stream_handle(device))
+            return
+        except _native.OrigamiNativeError as err:
+            if err.code != _native.ORIGAMI_ERR_UNSUPPORTED:
+                raise
+    for i, (flat, layout, tokens, _) in enumerate(reqs):  # irregular plans: one by one
+        unpack_to_kv_cache(flat, layout, int(tokens), kv_cache,
+                           dev_tables[int(bounds[i]):int(bounds[i + 1])])
+
+
 def scatter_kv_blocks(value: torch.Tensor, tokens: int, kv_cache: torch.Tensor,
                       block_ids: torch.Tensor) -> None:
     """Token-major K/V bytes [2, tokens, H, head_bytes] -> paged cache,

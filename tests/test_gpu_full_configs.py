@@ -13,7 +13,9 @@ Chunks come from the planner at 1 MiB (chunking.py:22-123).  For every
 request the HIP pack from the paged cache must equal the oracle's pack of
 the gathered bytes, and the HIP restore into the destination cache must
 equal the oracle's unpack + scatter (benchmark_utils.py:350-444), over the
-whole cache, byte for byte."""
+whole cache, byte for byte.  For the two batches, the batched restore (one
+launch per layer, shared prefix blocks written once) must give the same
+cache."""
 import os
 
 import numpy as np
@@ -53,7 +55,7 @@ def _tables(perm, nblks, shared, pool):
     return out
 
 
-def _run(dev, H, D, dtype, lengths, seed, shared_pool, expect_chunks=None):
+def _run(dev, H, D, dtype, lengths, seed, shared_pool, expect_chunks=None, batch=False):
     esize = torch.empty((), dtype=dtype).element_size()
     C = D * esize
     rng = np.random.default_rng(seed)
@@ -71,6 +73,7 @@ def _run(dev, H, D, dtype, lengths, seed, shared_pool, expect_chunks=None):
     src_u8 = src.view(torch.uint8).cpu().numpy()
     expect = np.zeros_like(src_u8)
     layouts = {}
+    streams = []
     for T, st, dt in zip(lengths, src_tables, dst_tables):
         T = int(T)
         lay = layouts.setdefault(T, _layout(T, H, C))
@@ -85,9 +88,20 @@ def _run(dev, H, D, dtype, lengths, seed, shared_pool, expect_chunks=None):
         native_gpu.unpack_to_kv_cache(stream, lay, T, dst,
                                       native_gpu.block_ids_tensor(dt, dev, NB))
         oracle.restore_layer(flat, offs, 8, lay.specs, T, H, C, dt, expect)
+        if batch:
+            streams.append(stream)
         del flat, stream
     got = dst.view(torch.uint8).cpu().numpy()
     assert np.array_equal(got, expect), "restored cache differs from the oracle"
+    if batch:
+        # one launch per layer for the whole batch, shared prefix blocks once
+        dst.zero_()
+        native_gpu.unpack_batch_to_kv_cache(
+            [(s_, layouts[int(T)], int(T), dt) for s_, T, dt in zip(streams, lengths, dst_tables)],
+            dst, dedup_shared_blocks=shared_pool)
+        assert np.array_equal(dst.view(torch.uint8).cpu().numpy(), expect), \
+            "batched restore differs from the oracle"
+        del streams
     # and from the source blocks themselves (the prefix pool holds identical
     # bytes for every request that references it)
     for T, st, dt in zip(lengths, src_tables, dst_tables):
@@ -100,14 +114,15 @@ def _run(dev, H, D, dtype, lengths, seed, shared_pool, expect_chunks=None):
 def test_qwen25_7b_batch_full(cuda_device):
     lengths = np.random.default_rng(2).integers(8192, 65537, 8)
     assert not all(int(T) % 16 == 0 for T in lengths)  # ragged lengths are covered
-    NB, tables = _run(cuda_device, 4, 128, torch.bfloat16, lengths, 2, True)
+    NB, tables = _run(cuda_device, 4, 128, torch.bfloat16, lengths, 2, True, batch=True)
     # the destination prefix pool is referenced by every table
     k = min(int(T) // 2 // BS for T in lengths)
     assert all(np.array_equal(t[:k], tables[0][:k]) for t in tables)
 
 
 def test_llama3_8b_fp8_16x16k_full(cuda_device):
-    _run(cuda_device, 8, 128, torch.float8_e4m3fn, [16384] * 16, 3, False, expect_chunks=32)
+    _run(cuda_device, 8, 128, torch.float8_e4m3fn, [16384] * 16, 3, False, expect_chunks=32,
+         batch=True)
 
 
 def test_llama3_70b_131072_full(cuda_device):
