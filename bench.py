@@ -110,10 +110,14 @@ def main() -> int:
     gen.manual_seed(args.seed)
     src_cache = torch.empty((2, NB, bs, H, D), dtype=torch.bfloat16, device=dev)
     streams, dst_ids, dst_caches = [], [], []
+    src_tokens0 = None
     for layer in range(L):
         src_ids = torch.randperm(NB, generator=gen, device=dev)[:nblk].contiguous()
         fill_layer(src_cache, src_ids, gen)
         streams.append(native_gpu.pack_from_kv_cache(src_cache, src_ids, T, layout))
+        if layer == 0:  # layer 0's source tokens, for the check below
+            src_tokens0 = (src_cache.view(torch.uint8)[:, src_ids].reshape(2, -1, H * C)[:, :T]
+                           .contiguous())
         dst_ids.append(torch.randperm(NB, generator=gen, device=dev)[:nblk].contiguous())
         dst_caches.append(torch.zeros((2, NB, bs, H, D), dtype=torch.bfloat16, device=dev))
     torch.cuda.synchronize()
@@ -128,15 +132,16 @@ def main() -> int:
             native_gpu.unpack_to_kv_cache(streams[layer], layout, T, dst_caches[layer],
                                           dst_ids[layer])
 
-    # correctness spot check before timing: layer 0 gathered back == source
+    # correctness check before timing, independent of the kernels: layer 0's
+    # stream is the plane-major transpose of its source tokens and the
+    # restored blocks hold those tokens (b = 8 planner layout)
     restore_all()
     torch.cuda.synchronize()
-    back = native_gpu.gather_kv_blocks(dst_caches[0], dst_ids[0])
-    ref_stream = native_gpu.pack_layout(back.reshape(2, nblk * bs, H * C)[:, :T].contiguous()
-                                        .reshape(-1), layout)
-    if not torch.equal(ref_stream, streams[0]):
-        print("restore check failed: layer 0 does not round-trip", file=sys.stderr)
+    if bits == 8 and not _closed_form_ok(streams[0], src_tokens0,
+                                         dst_caches[0].view(torch.uint8), dst_ids[0], T, H, C):
+        print("restore check failed: layer 0 differs from its source tokens", file=sys.stderr)
         return 1
+    del src_tokens0
 
     for _ in range(args.warmup):
         restore_all()
@@ -346,16 +351,10 @@ def _planner_layout(T, H, C):
     return kv_symbol_layout(T, H, C, 8, specs)
 
 
-def _time_restores(items, dev, steps):
-    """ms per pass over `items` = [(stream, layout, tokens, cache, ids)], with
-    events on the launch stream, after two warm-up passes."""
+def _time_passes(one_pass, dev, steps):
+    """ms per call of one_pass(), with events on the launch stream, after two
+    warm-up calls."""
     import torch
-
-    from origami_amd.lossless import native_gpu
-
-    def one_pass():
-        for stream, layout, T, cache, ids in items:
-            native_gpu.unpack_to_kv_cache(stream, layout, T, cache, ids)
 
     for _ in range(2):
         one_pass()
@@ -370,40 +369,44 @@ def _time_restores(items, dev, steps):
     return e0.elapsed_time(e1) / steps
 
 
-def _restore_round_trips(items):
-    """Every request restored into its blocks re-packs to its stream."""
+def _closed_form_ok(stream, src_tokens, cache, ids, T, H, C):
+    """Checks a b = 8 planner-layout restore without the kernels' own
+    inverse: the stream is the plane-major transpose of the source tokens
+    (plane h * C + c holds that channel's 2T symbols, K then V), and the
+    restored blocks hold the source tokens, zeros past T.  `src_tokens` is
+    uint8 [2, T, H * C]; `cache` a uint8 view of a [2, NB, bs, H, D] cache."""
     import torch
 
-    from origami_amd.lossless import native_gpu
-
-    for stream, layout, T, cache, ids in items:
-        H, C = layout.num_heads, layout.head_dim
-        back = native_gpu.gather_kv_blocks(cache, ids).view(torch.uint8)
-        back = back.reshape(2, -1, H * C)[:, :T].contiguous().reshape(-1)
-        if not torch.equal(native_gpu.pack_layout(back, layout), stream):
-            return False
-    return True
+    sym = src_tokens.reshape(2 * T, H * C)
+    if not torch.equal(stream.view(H * C, 2 * T), sym.t()):
+        return False
+    got = cache[:, ids].reshape(2, -1, H * C)
+    return bool(torch.equal(got[:, :T], src_tokens)) and not bool(got[:, T:].any())
 
 
 def configs_leg(dev, steps, layers):
     """Restore throughput at the other KV geometries, `layers` layers each
-    (every layer has its own paged cache and streams; a pass restores every
-    request of every layer, one fused launch per request and layer):
+    (every layer has its own paged cache and streams):
 
     * qwen2.5-7b-batch: 4 KV heads, head_dim 128, bf16, bs 16; 8 requests of
       U[8192, 65536] tokens (seed 2) whose first floor(T/2/bs) blocks come
       from a prefix pool shared by all block tables (the same destination
-      blocks are written by several requests); bytes are reported counting
-      each destination block once (`gbps`) and per write (`gbps_with_repeats`);
+      blocks in every request).  One batched launch per layer; a shared
+      prefix block is read and written once.  Bytes count what the job needs:
+      each request's stream except its shared-prefix blocks past the first
+      occurrence, each destination block once, the tables (`gbps`);
+      `gbps_with_repeats` counts every request's full stream and blocks;
     * llama3-8b-fp8-16x16k: 8 KV heads, head_dim 128, float8_e4m3fn (128-byte
-      head rows), 16 requests of 16384 tokens;
+      head rows), 16 requests of 16384 tokens, one batched launch per layer;
     * llama3-70b-128k: 8 KV heads, head_dim 128, bf16, one 131072-token
       request per layer;
     * llama3-8b-4k: one layer of one 4096-token request, 8 KV heads,
       head_dim 128, bf16, block table 0..255 (a launch-bound size).
 
     All use 1 MiB planner chunks and bits 8; the tables are permuted except
-    for the 4096-token case."""
+    for the 4096-token case.  For the batches, `per_request_us` times the
+    same layers restored one launch per request.  Each geometry's last layer
+    is checked in closed form (_closed_form_ok)."""
     import numpy as np
     import torch
 
@@ -413,65 +416,106 @@ def configs_leg(dev, steps, layers):
     bs = 16
     out = {}
 
-    def build(name, H, D, dtype, lengths, seed, shared_pool, identity=False, nlayers=layers):
+    def build(name, H, D, dtype, lengths, seed, shared_pool, identity=False, nlayers=layers,
+              batch=False):
         esize = torch.empty((), dtype=dtype).element_size()
         C = D * esize
         rng = np.random.default_rng(seed)
         gen = torch.Generator(device=dev)
         gen.manual_seed(seed)
-        nblks = [-(-int(T) // bs) for T in lengths]
-        pool = max(int(T) // 2 // bs for T in lengths) if shared_pool else 0
-        shared = [int(T) // 2 // bs if shared_pool else 0 for T in lengths]
+        lengths = [int(T) for T in lengths]
+        nblks = [-(-T // bs) for T in lengths]
+        pool = max(T // 2 // bs for T in lengths) if shared_pool else 0
+        shared = [T // 2 // bs if shared_pool else 0 for T in lengths]
         NB = pool + sum(n - k for n, k in zip(nblks, shared)) + 64
-        layouts = {int(T): _planner_layout(int(T), H, C) for T in set(lengths)}
+        layouts = {T: _planner_layout(T, H, C) for T in set(lengths)}
         src = torch.zeros((2, NB, bs, H, D), dtype=dtype, device=dev)
-        items, alg_unique, alg_repeats = [], 0, 0
-        for _ in range(nlayers):
+        layers_items, alg_unique, alg_repeats, ok = [], 0, 0, True
+        batches = []
+
+        def tables():
+            perm = np.arange(NB) if identity else rng.permutation(NB)
+            cur, ts = pool, []
+            for n, k in zip(nblks, shared):
+                ts.append(np.concatenate([perm[:k], perm[cur:cur + n - k]]).astype(np.int64))
+                cur += n - k
+            return ts
+
+        for layer in range(nlayers):
             fill_layer(src, torch.arange(NB, device=dev), gen)
-
-            def tables():
-                perm = np.arange(NB) if identity else rng.permutation(NB)
-                cur, ts = pool, []
-                for n, k in zip(nblks, shared):
-                    ts.append(np.concatenate([perm[:k], perm[cur:cur + n - k]]).astype(np.int64))
-                    cur += n - k
-                return ts
-
+            src_tables, dst_tables = tables(), tables()
             cache = torch.zeros((2, NB, bs, H, D), dtype=dtype, device=dev)
-            for T, st, dt in zip(lengths, tables(), tables()):
-                lay = layouts[int(T)]
-                stream = native_gpu.pack_from_kv_cache(src, native_gpu.block_ids_tensor(st, dev, NB),
-                                                       int(T), lay)
-                items.append((stream, lay, int(T), cache, native_gpu.block_ids_tensor(dt, dev, NB)))
-                alg_repeats += lay.stream_bytes + 2 * dt.size * bs * H * C + 8 * dt.size
-            written = len(np.unique(np.concatenate([it[4].cpu().numpy() for it in items
-                                                    if it[3] is cache])))
-            alg_unique += (sum(it[1].stream_bytes + 8 * it[4].numel() for it in items
-                               if it[3] is cache) + 2 * written * bs * H * C)
+            reqs = []
+            for T, st, dt in zip(lengths, src_tables, dst_tables):
+                stream = native_gpu.pack_from_kv_cache(
+                    src, native_gpu.block_ids_tensor(st, dev, NB), T, layouts[T])
+                reqs.append((stream, layouts[T], T, dt))
+            rb = native_gpu.KVRestoreBatch([r[1] for r in reqs], lengths,
+                                           [r[3] for r in reqs], cache,
+                                           dedup_shared_blocks=shared_pool)
+            batches.append(rb)
+            ids_dev = [native_gpu.block_ids_tensor(dt, dev, NB) for dt in dst_tables]
+            layers_items.append((reqs, cache, ids_dev))
+            stream_bytes = sum(r[1].stream_bytes for r in reqs)
+            table_bytes = 8 * sum(r[3].size for r in reqs)
+            written = len(np.unique(np.concatenate(dst_tables)))
+            # a skipped (shared) block is neither read nor written again
+            skipped_read = rb.skipped_blocks * 2 * bs * H * C
+            alg_unique += stream_bytes - skipped_read + 2 * written * bs * H * C + table_bytes
+            alg_repeats += stream_bytes + 2 * sum(nblks) * bs * H * C + table_bytes
+            if layer == nlayers - 1:
+                # closed-form check of this layer (restored once up front)
+                if batch:
+                    rb.restore([r[0] for r in reqs], cache)
+                else:
+                    for (stream, lay, T, _), ids in zip(reqs, ids_dev):
+                        native_gpu.unpack_to_kv_cache(stream, lay, T, cache, ids)
+                cu8 = cache.view(torch.uint8)
+                su8 = src.view(torch.uint8)
+                for (stream, lay, T, dt), st in zip(reqs, src_tables):
+                    tok = su8[:, torch.from_numpy(st).to(dev)].reshape(2, -1, H * C)[:, :T]
+                    ok = ok and _closed_form_ok(stream, tok.contiguous(), cu8,
+                                                torch.from_numpy(dt).to(dev), T, H, C)
         del src
-        ms = _time_restores(items, dev, steps)
-        ok = _restore_round_trips(items[-len(lengths):])
+
+        def batched_pass():
+            for rb, (reqs, cache, _) in zip(batches, layers_items):
+                rb.restore([r[0] for r in reqs], cache)
+
+        def per_request_pass():
+            for reqs, cache, ids_dev in layers_items:
+                for (stream, lay, T, _), ids in zip(reqs, ids_dev):
+                    native_gpu.unpack_to_kv_cache(stream, lay, T, cache, ids)
+
+        ms = _time_passes(batched_pass if batch else per_request_pass, dev, steps)
         res = {
             "layers": nlayers, "requests_per_layer": len(lengths),
-            "tokens_per_layer": int(sum(int(T) for T in lengths)),
+            "tokens_per_layer": int(sum(lengths)),
             "kv_heads": H, "head_dim": D, "kv_dtype": str(dtype).replace("torch.", ""),
+            "launch": ("one batched launch per layer" if batch
+                       else "one launch per request and layer"),
             "per_layer_us": round(1e3 * ms / nlayers, 2),
             "algorithmic_bytes_per_layer": int(alg_unique // nlayers),
             "gbps": round(alg_unique / (ms * 1e-3) / 1e9, 2),
             "frac": round(alg_unique / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "restore_ok": ok,
+            "restore_ok": bool(ok),
         }
+        if batch:
+            ms_req = _time_passes(per_request_pass, dev, steps)
+            res["per_request_us"] = round(1e3 * ms_req / nlayers, 2)
         if shared_pool:
             res["gbps_with_repeats"] = round(alg_repeats / (ms * 1e-3) / 1e9, 2)
             res["algorithmic_bytes_per_layer_with_repeats"] = int(alg_repeats // nlayers)
+            res["shared_blocks_skipped_per_layer"] = int(batches[0].skipped_blocks)
         out[name] = res
-        del items
+        del layers_items, batches
         torch.cuda.empty_cache()
 
     build("llama3-8b-4k", 8, 128, torch.bfloat16, [4096], 0, False, identity=True, nlayers=1)
     lengths = np.random.default_rng(2).integers(8192, 65537, 8)
-    build("qwen2.5-7b-batch", 4, 128, torch.bfloat16, lengths, 2, True)
-    build("llama3-8b-fp8-16x16k", 8, 128, torch.float8_e4m3fn, [16384] * 16, 3, False)
+    build("qwen2.5-7b-batch", 4, 128, torch.bfloat16, lengths, 2, True, batch=True)
+    build("llama3-8b-fp8-16x16k", 8, 128, torch.float8_e4m3fn, [16384] * 16, 3, False,
+          batch=True)
     build("llama3-70b-128k", 8, 128, torch.bfloat16, [131072], 4, False)
     return out
 

@@ -56,9 +56,6 @@ typedef struct ihipStream_t* origami_stream_t; /* == hipStream_t */
 #define ORIGAMI_CACHE_KV_FIRST 0
 #define ORIGAMI_CACHE_BLOCKS_FIRST 1
 
-/* origami_unpack_canonical_to_kv_cache_batch flags */
-#define ORIGAMI_BATCH_SKIP_UNWRITTEN 1 /* read nothing for destination blocks that are skipped */
-
 /* element types of dequantize inputs and outputs */
 #define ORIGAMI_DTYPE_FLOAT16 1
 #define ORIGAMI_DTYPE_BFLOAT16 2
@@ -205,11 +202,12 @@ int origami_unpack_canonical_to_kv_cache_noalloc(
  * unpack + copy_kv_to_hbm per request and layer).  The requests of one call
  * run concurrently: two requests must not carry different bytes for the same
  * destination block (vLLM's shared prefix blocks hold the same bytes).  Block
- * ids outside [0, num_blocks) are skipped, as in the single restore; with
- * ORIGAMI_BATCH_SKIP_UNWRITTEN (block_size a multiple of 16) the stream bytes
- * of a skipped block are not read either, so a caller can write a shared
- * prefix block once by passing -1 for its later occurrences.  All requests
- * are validated before anything is launched.
+ * ids outside [0, num_blocks) are skipped, as in the single restore.
+ * first_tokens (NULL: all 0) starts request r at destination token
+ * first_tokens[r], a multiple of block_size and of 16: its earlier blocks are
+ * neither read nor written, so a shared prefix that an earlier request of
+ * the batch restores is moved once.  All requests are validated before
+ * anything is launched.
  */
 int origami_unpack_canonical_to_kv_cache_batch(
     int64_t num_requests, const uint8_t* const* flat_chunks, const int64_t* flat_bytes,
@@ -217,7 +215,7 @@ int origami_unpack_canonical_to_kv_cache_batch(
     const int64_t* const* chunk_specs, const int64_t* num_chunks, const int64_t* tokens,
     void* kv_cache, int64_t cache_layout, int64_t num_blocks, int64_t block_size,
     int64_t num_heads, int64_t head_bytes, const int64_t* const* block_ids,
-    const int64_t* block_counts, int64_t flags, origami_stream_t stream);
+    const int64_t* block_counts, const int64_t* first_tokens, origami_stream_t stream);
 
 /*
  * Fused save: gather a layer's K/V through the block table from the paged

@@ -26,8 +26,6 @@ DTYPE_FLOAT16 = 1
 DTYPE_BFLOAT16 = 2
 DTYPE_FLOAT32 = 3
 
-BATCH_SKIP_UNWRITTEN = 1
-
 KIVI_PACKED_LSB = 0
 KIVI_NIBBLE3 = 1
 
@@ -49,7 +47,7 @@ _SIGNATURES: dict[str, list] = {
     "origami_unpack_canonical_to_kv_cache_noalloc": [
         _p, _i64, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "origami_unpack_canonical_to_kv_cache_batch": [
-        _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p],
+        _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p],
     "origami_pack_canonical_from_kv_cache": [
         _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _i64, _p],
     "origami_scatter_kv_blocks": [_p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],

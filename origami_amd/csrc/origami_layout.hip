@@ -447,8 +447,7 @@ struct RowsParams {
   int32_t nqt;               // workgroups along channels
   int32_t nst;               // workgroups along tokens
   int64_t ntiles;            // workgroup tiles; a workgroup loops over tiles
-  int32_t skip_dead;         // unpack: a lane whose destination block id is outside
-                             // [0, num_blocks) reads nothing (bs a multiple of 16)
+  int64_t token0;            // first destination token of the tiles (a multiple of 16)
 };
 
 // Per-request fields of a batched restore (one layer of several requests
@@ -460,9 +459,9 @@ struct RowsRequest {
   int64_t plane_base, plane_bits;
   const int64_t* block_ids;
   int64_t T, row_tokens;
-  int64_t tile0;  // first workgroup tile of the request
+  int64_t token0;  // tokens [token0, row_tokens) are restored
+  int64_t tile0;   // first workgroup tile of the request
   int32_t nst;
-  int32_t skip_dead;
 };
 
 constexpr int kBatchRequests = 16;  // requests per batched launch (kernel arguments)
@@ -724,7 +723,7 @@ __device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, int64_t til
   const int wqi = wave % p.wq, wsi = wave / p.wq;
   tc.slot = wqi * kLaneGroups + (lane >> 3);
   tc.q = qt * p.wq * kLaneGroups + tc.slot;
-  tc.t0 = (static_cast<int64_t>(st * p.ws + wsi) * kLaneSegs + (lane & 7)) * kSegTokens;
+  tc.t0 = p.token0 + (static_cast<int64_t>(st * p.ws + wsi) * kLaneSegs + (lane & 7)) * kSegTokens;
   return tc;
 }
 
@@ -788,14 +787,8 @@ __device__ __forceinline__ void unpack_tile(const RowsParams& p, int64_t tile,
                                             const int64_t* desc) {
   const TileCoord tc = tile_coord(p, tile);
   if (tc.q >= p.nq || tc.t0 >= p.row_tokens) return;
-  int64_t nv = p.T - tc.t0;  // tokens of this segment that hold symbols
+  const int64_t nv = p.T - tc.t0;  // tokens of this segment that hold symbols
   const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
-  if (p.skip_dead) {
-    // the lane's 16 tokens lie in one block (bs % 16 == 0): an id outside the
-    // cache means nothing of the segment is written, so nothing is read
-    const int64_t pid = p.block_ids[tc.t0 / p.bs];
-    if (pid < 0 || pid >= p.num_blocks) nv = 0;
-  }
 
   uint32_t v[16][4];
 #pragma unroll
@@ -868,7 +861,7 @@ __global__ __launch_bounds__(kRowsThreads) void rows_unpack_batch_kernel(RowsBat
     p.T = q.T;
     p.row_tokens = q.row_tokens;
     p.nst = q.nst;
-    p.skip_dead = q.skip_dead;
+    p.token0 = q.token0;
     const int64_t local = tile - q.tile0;
     load_descriptors(p, local, desc);
     unpack_tile<BITS, MODE>(p, local, desc);
@@ -1187,12 +1180,13 @@ void set_batch_grid(RowsBatch& b, int64_t H, int64_t C) {
     p.ws = waves / wq;
     p.nqt = (nqg + wq - 1) / wq;
     int64_t tiles = 0;
-    for (int r = 0; r < b.nreq; ++r) tiles += 2 * H * p.nqt * nst_of(b.req[r].row_tokens);
+    for (int r = 0; r < b.nreq; ++r)
+      tiles += 2 * H * p.nqt * nst_of(b.req[r].row_tokens - b.req[r].token0);
     if (tiles >= want || waves == 4) break;
   }
   int64_t tile0 = 0;
   for (int r = 0; r < b.nreq; ++r) {
-    b.req[r].nst = static_cast<int32_t>(nst_of(b.req[r].row_tokens));
+    b.req[r].nst = static_cast<int32_t>(nst_of(b.req[r].row_tokens - b.req[r].token0));
     b.req[r].tile0 = tile0;
     tile0 += 2 * H * p.nqt * static_cast<int64_t>(b.req[r].nst);
   }
@@ -1716,13 +1710,9 @@ int origami_unpack_canonical_to_kv_cache_batch(
     const int64_t* const* chunk_specs, const int64_t* num_chunks, const int64_t* tokens,
     void* kv_cache, int64_t cache_layout, int64_t num_blocks, int64_t block_size,
     int64_t num_heads, int64_t head_bytes, const int64_t* const* block_ids,
-    const int64_t* block_counts, int64_t flags, origami_stream_t stream_) {
+    const int64_t* block_counts, const int64_t* first_tokens, origami_stream_t stream_) {
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   ORIGAMI_REQUIRE(num_requests >= 0, "request count must be non-negative");
-  ORIGAMI_REQUIRE((flags & ~int64_t(ORIGAMI_BATCH_SKIP_UNWRITTEN)) == 0, "unknown batch flags");
-  const bool skip = (flags & ORIGAMI_BATCH_SKIP_UNWRITTEN) != 0;
-  ORIGAMI_REQUIRE(!skip || block_size % 16 == 0,
-                  "skipping unwritten blocks needs a block size that is a multiple of 16");
   // validate and plan every request before anything is launched
   struct Item {
     RowsRequest q;
@@ -1760,7 +1750,12 @@ int origami_unpack_canonical_to_kv_cache_batch(
     it.q.block_ids = p.block_ids;
     it.q.T = p.T;
     it.q.row_tokens = p.row_tokens;
-    it.q.skip_dead = skip ? 1 : 0;
+    const int64_t first = first_tokens ? first_tokens[r] : 0;
+    ORIGAMI_REQUIRE(first >= 0 && first <= p.row_tokens,
+                    "first_tokens must lie in [0, block_count * block_size]");
+    ORIGAMI_REQUIRE(first % 16 == 0 && first % block_size == 0,
+                    "first_tokens must be a multiple of the block size and of 16");
+    it.q.token0 = first;
     it.bits = plan->info.bits;
     it.mode = rows_mode(plan->info, p, tokens[r], false);
     items.push_back(it);

@@ -339,73 +339,116 @@ def batch_block_tables(block_tables: Sequence, tokens: Sequence[int], block_size
     return tables, True
 
 
+class KVRestoreBatch:
+    """One layer of several requests restored into a cache per call, the
+    block tables prepared once for all layers of the batch.  The reference
+    restores request by request (worker.py:796-897 and 1087-1248); here each
+    layer is one native call and one launch per symbol width and addressing
+    mode.  `layouts[r]`, `tokens[r]` and `block_tables[r]` (host ids) describe
+    request r; the result of restore() equals restoring the requests one
+    after another.  With `dedup_shared_blocks` a full block shared by several
+    requests (vLLM prefix blocks hold the same bytes) is written once, from the
+    first request that has it; a later request's leading shared blocks are
+    not read either.  restore() is not safe to call concurrently on one
+    object."""
+
+    def __init__(self, layouts: Sequence[CanonicalLayout], tokens: Sequence[int],
+                 block_tables: Sequence, kv_cache: torch.Tensor, *,
+                 dedup_shared_blocks: bool = False):
+        _require_cuda(kv_cache, "kv_cache")
+        self.geometry = cache_geometry(kv_cache)
+        self.device = kv_cache.device
+        code, nb, bs, H, head_bytes = self.geometry
+        self.layouts = list(layouts)
+        self.tokens = [int(t) for t in tokens]
+        if not (len(self.layouts) == len(self.tokens) == len(block_tables)):
+            raise RuntimeError("layouts, tokens and block tables must have one entry per request")
+        for layout, T in zip(self.layouts, self.tokens):
+            if (layout.token_count != 2 * T or layout.num_heads != H
+                    or layout.head_dim != head_bytes):
+                raise RuntimeError("symbol layout does not match the kv_cache geometry")
+        host = []
+        for ids in block_tables:
+            ids_np = (ids.detach().to("cpu", torch.int64).numpy()
+                      if isinstance(ids, torch.Tensor) else np.asarray(ids, dtype=np.int64))
+            ids_np = ids_np.reshape(-1)
+            if ids_np.size == 0:
+                raise RuntimeError("block_ids must be non-empty")
+            if int(ids_np.min()) < 0 or int(ids_np.max()) >= nb:
+                raise RuntimeError("block id out of range for kv_cache")
+            host.append(ids_np)
+        dedup = bool(dedup_shared_blocks) and bs % 16 == 0
+        tables, self.batchable = batch_block_tables(host, self.tokens, bs, dedup)
+        # a request's leading shared blocks are not read or written at all
+        # (its restore starts past them); other shared blocks are skipped on
+        # write (ids -1)
+        lead = []
+        for t in tables:
+            live = np.flatnonzero(t >= 0)
+            lead.append(int(live[0]) if live.size else int(t.size))
+        self.skipped_blocks = int(sum(lead))
+        self._first = np.ascontiguousarray(np.asarray([k * bs for k in lead], dtype=np.int64))
+        self.block_counts = [int(t.size) for t in tables]
+        n = len(tables)
+        if n:
+            self._dev_tables = torch.from_numpy(np.concatenate(tables)).to(self.device)
+        bounds = np.cumsum([0] + self.block_counts)
+        self.tables = [self._dev_tables[int(bounds[i]):int(bounds[i + 1])] for i in range(n)]
+        u64 = lambda vals: np.ascontiguousarray(np.asarray(vals, dtype=np.uint64))  # noqa: E731
+        i64 = lambda vals: np.ascontiguousarray(np.asarray(vals, dtype=np.int64))  # noqa: E731
+        self._offs = u64([lay.offsets.ctypes.data for lay in self.layouts])
+        self._bits = u64([lay.bits.ctypes.data for lay in self.layouts])
+        self._specs = u64([lay.specs.ctypes.data for lay in self.layouts])
+        self._nchunks = i64([lay.num_chunks for lay in self.layouts])
+        self._tok = i64(self.tokens)
+        self._ids = u64([t.data_ptr() for t in self.tables])
+        self._counts = i64(self.block_counts)
+        self._flats = np.zeros(n, dtype=np.uint64)
+        self._flat_bytes = np.zeros(n, dtype=np.int64)
+
+    def restore(self, flats: Sequence[torch.Tensor], kv_cache: torch.Tensor) -> None:
+        """Restores one layer: flats[r] is request r's stream on the device."""
+        if len(flats) != len(self.layouts):
+            raise RuntimeError("one stream per request is required")
+        if cache_geometry(kv_cache) != self.geometry or kv_cache.device != self.device:
+            raise RuntimeError("kv_cache geometry differs from the prepared batch")
+        if not self.layouts:
+            return
+        if not self.batchable:
+            for flat, layout, T, ids in zip(flats, self.layouts, self.tokens, self.tables):
+                unpack_to_kv_cache(flat, layout, T, kv_cache, ids)
+            return
+        for i, flat in enumerate(flats):
+            _require_cuda(flat, "flat_chunks")
+            self._flats[i] = flat.data_ptr()
+            self._flat_bytes[i] = flat.numel()
+        code, nb, bs, H, head_bytes = self.geometry
+        with _device_guard(self.device):
+            try:
+                _native.call(
+                    "origami_unpack_canonical_to_kv_cache_batch", len(flats),
+                    self._flats.ctypes.data, self._flat_bytes.ctypes.data, self._offs.ctypes.data,
+                    self._bits.ctypes.data, self._specs.ctypes.data, self._nchunks.ctypes.data,
+                    self._tok.ctypes.data, kv_cache.data_ptr(), code, nb, bs, H, head_bytes,
+                    self._ids.ctypes.data, self._counts.ctypes.data, self._first.ctypes.data,
+                    _stream_handle(self.device))
+                return
+            except _native.OrigamiNativeError as err:
+                if err.code != _native.ORIGAMI_ERR_UNSUPPORTED:
+                    raise
+        for flat, layout, T, ids in zip(flats, self.layouts, self.tokens, self.tables):
+            unpack_to_kv_cache(flat, layout, T, kv_cache, ids)  # irregular plans
+
+
 def unpack_batch_to_kv_cache(requests: Sequence[tuple], kv_cache: torch.Tensor, *,
                              dedup_shared_blocks: bool = False) -> None:
-    """Fused restore of one layer of several requests into one cache, in one
-    launch per symbol width and addressing mode (the reference restores
-    request by request, worker.py:796-897 and 1087-1248).  `requests` holds
-    (flat stream, kv_symbol_layout, tokens, block ids) per request, block ids
-    as a host sequence.  The result equals restoring the requests one after
-    another; with `dedup_shared_blocks` a full block shared by several requests
-    is read and written once."""
-    _require_cuda(kv_cache, "kv_cache")
-    code, nb, bs, H, head_bytes = cache_geometry(kv_cache)
+    """One layer of several requests, (flat stream, kv_symbol_layout, tokens,
+    host block ids) each, restored into one cache (KVRestoreBatch for a
+    single layer)."""
     reqs = list(requests)
-    if not reqs:
-        return
-    for flat, layout, tokens, _ in reqs:
-        _require_cuda(flat, "flat_chunks")
-        if (layout.token_count != 2 * int(tokens) or layout.num_heads != H
-                or layout.head_dim != head_bytes):
-            raise RuntimeError("symbol layout does not match the kv_cache geometry")
-    host_tables = []
-    for _, _, tokens, ids in reqs:
-        ids_np = (ids.detach().to("cpu", torch.int64).numpy() if isinstance(ids, torch.Tensor)
-                  else np.asarray(ids, dtype=np.int64))
-        if ids_np.size == 0:
-            raise RuntimeError("block_ids must be non-empty")
-        if int(ids_np.min()) < 0 or int(ids_np.max()) >= nb:
-            raise RuntimeError("block id out of range for kv_cache")
-        host_tables.append(ids_np)
-    tables, batchable = batch_block_tables(host_tables, [int(r[2]) for r in reqs], bs,
-                                           dedup_shared_blocks and bs % 16 == 0)
-    device = kv_cache.device
-    if not batchable:
-        for (flat, layout, tokens, _), t in zip(reqs, tables):
-            unpack_to_kv_cache(flat, layout, int(tokens), kv_cache,
-                               torch.from_numpy(t).to(device))
-        return
-    dev_tables = torch.from_numpy(np.concatenate(tables)).to(device)
-    bounds = np.cumsum([0] + [t.size for t in tables])
-    n = len(reqs)
-    ptr = lambda vals: np.ascontiguousarray(np.asarray(vals, dtype=np.uint64))  # noqa: E731
-    i64 = lambda vals: np.ascontiguousarray(np.asarray(vals, dtype=np.int64))  # noqa: E731
-    flats = ptr([r[0].data_ptr() for r in reqs])
-    flat_bytes = i64([r[0].numel() for r in reqs])
-    offs = ptr([r[1].offsets.ctypes.data for r in reqs])
-    bits = ptr([r[1].bits.ctypes.data for r in reqs])
-    specs = ptr([r[1].specs.ctypes.data for r in reqs])
-    nchunks = i64([r[1].num_chunks for r in reqs])
-    toks = i64([int(r[2]) for r in reqs])
-    base = dev_tables.data_ptr()
-    ids_ptrs = ptr([base + 8 * int(bounds[i]) for i in range(n)])
-    counts = i64([t.size for t in tables])
-    flags = _native.BATCH_SKIP_UNWRITTEN if dedup_shared_blocks and bs % 16 == 0 else 0
-    with _device_guard(device):
-        try:
-            _native.call(
-                "origami_unpack_canonical_to_kv_cache_batch", n, flats.ctypes.data,
-                flat_bytes.ctypes.data, offs.ctypes.data, bits.ctypes.data, specs.ctypes.data,
-                nchunks.ctypes.data, toks.ctypes.data, kv_cache.data_ptr(), code, nb, bs, H,
-                head_bytes, ids_ptrs.ctypes.data, counts.ctypes.data, flags,
-                _stream_handle(device))
-            return
-        except _native.OrigamiNativeError as err:
-            if err.code != _native.ORIGAMI_ERR_UNSUPPORTED:
-                raise
-    for i, (flat, layout, tokens, _) in enumerate(reqs):  # irregular plans: one by one
-        unpack_to_kv_cache(flat, layout, int(tokens), kv_cache,
-                           dev_tables[int(bounds[i]):int(bounds[i + 1])])
+    batch = KVRestoreBatch([r[1] for r in reqs], [r[2] for r in reqs], [r[3] for r in reqs],
+                           kv_cache, dedup_shared_blocks=dedup_shared_blocks)
+    batch.restore([r[0] for r in reqs], kv_cache)
 
 
 def scatter_kv_blocks(value: torch.Tensor, tokens: int, kv_cache: torch.Tensor,

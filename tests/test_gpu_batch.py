@@ -35,7 +35,7 @@ def _tables(rng, NB, nblks, shared):
 
 
 def _run(dev, rng, lengths, H, C, bits, bs, blocks_first, shared_frac, dedup,
-         partial_conflict=False):
+         partial_conflict=False, interior_share=False):
     nblks = [-(-int(T) // bs) for T in lengths]
     shared = [int(int(T) * shared_frac) // bs for T in lengths]
     NB = sum(nblks) + 16
@@ -46,11 +46,19 @@ def _run(dev, rng, lengths, H, C, bits, bs, blocks_first, shared_frac, dedup,
         dst_tables[1][-1] = dst_tables[0][-1 if int(lengths[0]) % bs == 0 else 0]
     # prefix bytes are the same in every request that shares the prefix
     prefix_sym = rng.integers(0, 256, (2, max(shared + [0]) * bs, H, C), dtype=np.uint8)
+    shared_mid = None
+    if interior_share:
+        # block 3 of request 1 is block 5 of request 0, with the same bytes
+        dst_tables[1][3] = dst_tables[0][5]
+        shared_mid = rng.integers(0, 256, (2, bs, H, C), dtype=np.uint8)
     items, host = [], []
-    for T, k in zip(lengths, shared):
+    for i, (T, k) in enumerate(zip(lengths, shared)):
         T = int(T)
         sym = rng.integers(0, 256, (2, T, H, C), dtype=np.uint8)
         sym[:, :k * bs] = prefix_sym[:, :k * bs]
+        if shared_mid is not None and i in (0, 1):
+            at = (5 if i == 0 else 3) * bs
+            sym[:, at:at + bs] = shared_mid
         lay = _layout(T, H, C, bits)
         flat, offs = oracle.pack_canonical(sym.reshape(-1), bits, lay.specs, [2 * T, H, C],
                                            [0, 1, 2, -1])
@@ -98,6 +106,13 @@ def test_batch_shared_partial_block_falls_back_in_order(cuda_device):
     rng = np.random.default_rng(9)
     lengths = [640, 1000, 300]
     _run(cuda_device, rng, lengths, 4, 256, 8, 16, False, 0.0, True, partial_conflict=True)
+
+
+@pytest.mark.parametrize("dedup", [False, True])
+def test_batch_interior_shared_block(cuda_device, dedup):
+    rng = np.random.default_rng(17)
+    _run(cuda_device, rng, [800, 500, 333], 4, 256, 8, 16, False, 0.0, dedup,
+         interior_share=True)
 
 
 def test_batch_fp8_sized_rows(cuda_device):
