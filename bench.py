@@ -487,7 +487,9 @@ def configs_leg(dev, steps, layers):
                 for (stream, lay, T, _), ids in zip(reqs, ids_dev):
                     native_gpu.unpack_to_kv_cache(stream, lay, T, cache, ids)
 
-        ms = _time_passes(batched_pass if batch else per_request_pass, dev, steps)
+        # at least ~200 launches per timing, so short layers reach steady state
+        passes = max(steps, -(-200 // (nlayers * (1 if batch else len(lengths)))))
+        ms = _time_passes(batched_pass if batch else per_request_pass, dev, passes)
         res = {
             "layers": nlayers, "requests_per_layer": len(lengths),
             "tokens_per_layer": int(sum(lengths)),
@@ -501,7 +503,7 @@ def configs_leg(dev, steps, layers):
             "restore_ok": bool(ok),
         }
         if batch:
-            ms_req = _time_passes(per_request_pass, dev, steps)
+            ms_req = _time_passes(per_request_pass, dev, passes)
             res["per_request_us"] = round(1e3 * ms_req / nlayers, 2)
         if shared_pool:
             res["gbps_with_repeats"] = round(alg_repeats / (ms * 1e-3) / 1e9, 2)

@@ -115,6 +115,22 @@ class CanonicalLayout:
         return int(self.specs.shape[0])
 
     @cached_property
+    def torch_meta(self):
+        """(offsets, bits, specs) as host int64 tensors sharing the arrays'
+        memory, as the extension module's fused entry points take them."""
+        import torch
+
+        return (torch.from_numpy(self.offsets), torch.from_numpy(self.bits),
+                torch.from_numpy(self.specs))
+
+    @cached_property
+    def torch_shape_axes(self):
+        """(source shape, axis positions) as host int64 tensors."""
+        import torch
+
+        return torch.from_numpy(self.shape_arr), torch.from_numpy(self.axes)
+
+    @cached_property
     def native_args(self) -> tuple[int, int, int, int]:
         """(offsets, bits, specs) host addresses and the chunk count, as the
         C entry points take them; the arrays live as long as the layout."""

@@ -15,12 +15,12 @@ from __future__ import annotations
 import contextlib
 import ctypes
 from functools import lru_cache
-from typing import Any, Iterable, Sequence
+from typing import Iterable, Sequence
 
 import numpy as np
 import torch
 
-from origami_amd import _native
+from origami_amd import _ext, _native
 from origami_amd.layout import CanonicalLayout, kv_symbol_layout
 
 CACHE_KV_FIRST = _native.CACHE_KV_FIRST
@@ -58,6 +58,7 @@ def available() -> bool:
         return False
     try:
         _native.lib()
+        _ext.ext()
         return True
     except Exception:  # noqa: BLE001 - mirrors the reference's available()
         return False
@@ -102,7 +103,11 @@ def unpack_layout(flat: torch.Tensor, layout: CanonicalLayout,
     if flat.dtype != torch.uint8:
         raise RuntimeError("flat_chunks must be uint8")
     if out is None:
-        out = torch.empty((layout.symbol_count,), dtype=torch.uint8, device=flat.device)
+        offs, bits, specs = layout.torch_meta
+        shape, axes = layout.torch_shape_axes
+        return _ext.ext().unpack_canonical_storage_chunks_cuda(
+            flat, offs, bits, shape, axes, layout.token_count, layout.num_heads,
+            layout.head_dim, specs)
     _require_cuda(out, "output")
     with _device_guard(flat.device):
         _native.call(
@@ -122,14 +127,10 @@ def pack_layout(symbols: torch.Tensor, layout: CanonicalLayout,
         raise RuntimeError("symbols must be uint8")
     if out is None:
         out = torch.empty((layout.stream_bytes,), dtype=torch.uint8, device=symbols.device)
-    _require_cuda(out, "flat_chunks")
-    with _device_guard(symbols.device):
-        _native.call(
-            "origami_pack_canonical_storage_chunks",
-            symbols.data_ptr(), symbols.numel(), *_layout_args(layout),
-            _native.host_ptr(layout.shape_arr), len(layout.shape), _native.host_ptr(layout.axes),
-            layout.token_count, layout.num_heads, layout.head_dim,
-            out.data_ptr(), out.numel(), _stream_handle(symbols.device))
+    shape, axes = layout.torch_shape_axes
+    _ext.ext().pack_canonical_storage_chunks(symbols, *layout.torch_meta, shape, axes,
+                                             layout.token_count, layout.num_heads,
+                                             layout.head_dim, out)
     return out
 
 
@@ -235,27 +236,17 @@ def unpack_to_kv_cache(flat: torch.Tensor, layout: CanonicalLayout, tokens: int,
     table.  `layout` is the [2*tokens, H, head_bytes] symbol layout of the
     layer (kv_symbol_layout).  Falls back to unpack + scatter (both on the
     GPU) when the chunk plan is not served by the fused kernel."""
-    _require_cuda(flat, "flat_chunks")
-    _require_cuda(kv_cache, "kv_cache")
-    _require_cuda(block_ids, "block_ids")
-    code, nb, bs, H, head_bytes = cache_geometry(kv_cache)
-    if layout.token_count != 2 * tokens or layout.num_heads != H or layout.head_dim != head_bytes:
+    if (layout.token_count != 2 * tokens or kv_cache.dim() != 5
+            or layout.num_heads != kv_cache.shape[3]
+            or layout.head_dim != kv_cache.shape[4] * kv_cache.element_size()):
         raise RuntimeError("symbol layout does not match the kv_cache geometry")
-    with _device_guard(kv_cache.device):
-        try:
-            _native.call(
-                "origami_unpack_canonical_to_kv_cache",
-                flat.data_ptr(), flat.numel(), *_layout_args(layout), int(tokens),
-                kv_cache.data_ptr(), code, nb, bs, H, head_bytes,
-                block_ids.data_ptr(), block_ids.numel(), _stream_handle(kv_cache.device))
-            return
-        except _native.OrigamiNativeError as err:
-            if err.code != _native.ORIGAMI_ERR_UNSUPPORTED:
-                raise
-        # Irregular chunk plan: unpack to the symbol tensor, then scatter.
-        symbols = unpack_layout(flat, layout) if layout.layout == ("token", "head", "head_dim") \
-            else _unpack_kv_tokens_major(flat, layout)
-        scatter_kv_blocks(symbols, tokens, kv_cache, block_ids)
+    if _ext.ext().unpack_canonical_to_kv_cache(flat, *layout.torch_meta, tokens, kv_cache,
+                                               block_ids):
+        return
+    # Irregular chunk plan: unpack to the symbol tensor, then scatter.
+    symbols = unpack_layout(flat, layout) if layout.layout == ("token", "head", "head_dim") \
+        else _unpack_kv_tokens_major(flat, layout)
+    scatter_kv_blocks(symbols, tokens, kv_cache, block_ids)
 
 
 def _unpack_kv_tokens_major(flat: torch.Tensor, layout: CanonicalLayout) -> torch.Tensor:
@@ -273,30 +264,20 @@ def pack_from_kv_cache(kv_cache: torch.Tensor, block_ids: torch.Tensor, tokens: 
     """Fused save of one layer: paged cache -> stream.  Falls back to gather +
     pack (both on the GPU) when the plan is not served by the fused kernel."""
     _require_cuda(kv_cache, "kv_cache")
-    _require_cuda(block_ids, "block_ids")
     code, nb, bs, H, head_bytes = cache_geometry(kv_cache)
     if layout.token_count != 2 * tokens or layout.num_heads != H or layout.head_dim != head_bytes:
         raise RuntimeError("symbol layout does not match the kv_cache geometry")
     if out is None:
         out = torch.empty((layout.stream_bytes,), dtype=torch.uint8, device=kv_cache.device)
-    with _device_guard(kv_cache.device):
-        try:
-            _native.call(
-                "origami_pack_canonical_from_kv_cache",
-                kv_cache.data_ptr(), code, nb, bs, H, head_bytes,
-                block_ids.data_ptr(), block_ids.numel(), int(tokens),
-                *_layout_args(layout), out.data_ptr(), out.numel(),
-                _stream_handle(kv_cache.device))
-            return out
-        except _native.OrigamiNativeError as err:
-            if err.code != _native.ORIGAMI_ERR_UNSUPPORTED:
-                raise
-        value = gather_kv_blocks(kv_cache, block_ids)
-        nblk_tokens = block_ids.numel() * bs
-        value = value.reshape(2, nblk_tokens, H * head_bytes)[:, :tokens].contiguous()
-        if layout.layout != ("token", "head", "head_dim"):
-            value = _tokens_major_to_layout(value.reshape(-1), layout)
-        return pack_layout(value.reshape(-1), layout, out)
+    if _ext.ext().pack_canonical_from_kv_cache(kv_cache, block_ids, int(tokens),
+                                               *layout.torch_meta, out):
+        return out
+    value = gather_kv_blocks(kv_cache, block_ids)
+    nblk_tokens = block_ids.numel() * bs
+    value = value.reshape(2, nblk_tokens, H * head_bytes)[:, :tokens].contiguous()
+    if layout.layout != ("token", "head", "head_dim"):
+        value = _tokens_major_to_layout(value.reshape(-1), layout)
+    return pack_layout(value.reshape(-1), layout, out)
 
 
 def _tokens_major_to_layout(value: torch.Tensor, layout: CanonicalLayout) -> torch.Tensor:
@@ -349,8 +330,7 @@ class KVRestoreBatch:
     after another.  With `dedup_shared_blocks` a full block shared by several
     requests (vLLM prefix blocks hold the same bytes) is written once, from the
     first request that has it; a later request's leading shared blocks are
-    not read either.  restore() is not safe to call concurrently on one
-    object."""
+    not read either."""
 
     def __init__(self, layouts: Sequence[CanonicalLayout], tokens: Sequence[int],
                  block_tables: Sequence, kv_cache: torch.Tensor, *,
@@ -358,6 +338,7 @@ class KVRestoreBatch:
         _require_cuda(kv_cache, "kv_cache")
         self.geometry = cache_geometry(kv_cache)
         self.device = kv_cache.device
+        self._shape, self._dtype = tuple(kv_cache.shape), kv_cache.dtype
         code, nb, bs, H, head_bytes = self.geometry
         self.layouts = list(layouts)
         self.tokens = [int(t) for t in tokens]
@@ -394,23 +375,17 @@ class KVRestoreBatch:
             self._dev_tables = torch.from_numpy(np.concatenate(tables)).to(self.device)
         bounds = np.cumsum([0] + self.block_counts)
         self.tables = [self._dev_tables[int(bounds[i]):int(bounds[i + 1])] for i in range(n)]
-        u64 = lambda vals: np.ascontiguousarray(np.asarray(vals, dtype=np.uint64))  # noqa: E731
-        i64 = lambda vals: np.ascontiguousarray(np.asarray(vals, dtype=np.int64))  # noqa: E731
-        self._offs = u64([lay.offsets.ctypes.data for lay in self.layouts])
-        self._bits = u64([lay.bits.ctypes.data for lay in self.layouts])
-        self._specs = u64([lay.specs.ctypes.data for lay in self.layouts])
-        self._nchunks = i64([lay.num_chunks for lay in self.layouts])
-        self._tok = i64(self.tokens)
-        self._ids = u64([t.data_ptr() for t in self.tables])
-        self._counts = i64(self.block_counts)
-        self._flats = np.zeros(n, dtype=np.uint64)
-        self._flat_bytes = np.zeros(n, dtype=np.int64)
+        self._offs = [lay.torch_meta[0] for lay in self.layouts]
+        self._bits = [lay.torch_meta[1] for lay in self.layouts]
+        self._specs = [lay.torch_meta[2] for lay in self.layouts]
+        self._first_list = [int(x) for x in self._first]
 
     def restore(self, flats: Sequence[torch.Tensor], kv_cache: torch.Tensor) -> None:
         """Restores one layer: flats[r] is request r's stream on the device."""
         if len(flats) != len(self.layouts):
             raise RuntimeError("one stream per request is required")
-        if cache_geometry(kv_cache) != self.geometry or kv_cache.device != self.device:
+        if tuple(kv_cache.shape) != self._shape or kv_cache.dtype != self._dtype \
+                or kv_cache.device != self.device:
             raise RuntimeError("kv_cache geometry differs from the prepared batch")
         if not self.layouts:
             return
@@ -418,24 +393,10 @@ class KVRestoreBatch:
             for flat, layout, T, ids in zip(flats, self.layouts, self.tokens, self.tables):
                 unpack_to_kv_cache(flat, layout, T, kv_cache, ids)
             return
-        for i, flat in enumerate(flats):
-            _require_cuda(flat, "flat_chunks")
-            self._flats[i] = flat.data_ptr()
-            self._flat_bytes[i] = flat.numel()
-        code, nb, bs, H, head_bytes = self.geometry
-        with _device_guard(self.device):
-            try:
-                _native.call(
-                    "origami_unpack_canonical_to_kv_cache_batch", len(flats),
-                    self._flats.ctypes.data, self._flat_bytes.ctypes.data, self._offs.ctypes.data,
-                    self._bits.ctypes.data, self._specs.ctypes.data, self._nchunks.ctypes.data,
-                    self._tok.ctypes.data, kv_cache.data_ptr(), code, nb, bs, H, head_bytes,
-                    self._ids.ctypes.data, self._counts.ctypes.data, self._first.ctypes.data,
-                    _stream_handle(self.device))
-                return
-            except _native.OrigamiNativeError as err:
-                if err.code != _native.ORIGAMI_ERR_UNSUPPORTED:
-                    raise
+        if _ext.ext().unpack_canonical_to_kv_cache_batch(
+                list(flats), self._offs, self._bits, self._specs, self.tokens, kv_cache,
+                self.tables, self._first_list):
+            return
         for flat, layout, T, ids in zip(flats, self.layouts, self.tokens, self.tables):
             unpack_to_kv_cache(flat, layout, T, kv_cache, ids)  # irregular plans
 
@@ -544,18 +505,13 @@ def cachegen_unpack_dequantize_to_kv_cache(
     if kv_cache.dtype not in (torch.float16, torch.bfloat16):
         raise RuntimeError("kv_cache must be float16 or bfloat16")
     max_key, max_value = max_key.contiguous(), max_value.contiguous()
-    max_code = _max_tensors(max_key, max_value)
+    _max_tensors(max_key, max_value)
     ids = block_ids.to(device=kv_cache.device, dtype=torch.int64).contiguous()
-    code, nb, bs = dequant_cache_geometry(kv_cache, heads, head_dim)
-    with _device_guard(kv_cache.device):
-        _native.call(
-            "origami_cachegen_unpack_dequantize_to_kv_cache",
-            flat.data_ptr(), flat.numel(), int(key_offset), int(key_bytes), int(value_offset),
-            int(value_bytes), int(key_bits), int(value_bits), int(key_bins), int(value_bins),
-            max_key.data_ptr(), max_value.data_ptr(), max_key.numel(), max_value.numel(),
-            max_code, kv_cache.data_ptr(), _DTYPE_CODES[kv_cache.dtype], code, nb, bs,
-            ids.data_ptr(), ids.numel(), int(tokens), int(heads), int(head_dim),
-            _stream_handle(kv_cache.device))
+    dequant_cache_geometry(kv_cache, heads, head_dim)
+    _ext.ext().cachegen_unpack_dequantize_to_kv_cache_cuda(
+        flat, int(key_offset), int(key_bytes), int(value_offset), int(value_bytes),
+        int(key_bits), int(value_bits), int(key_bins), int(value_bins), max_key, max_value,
+        kv_cache, ids, int(tokens), int(heads), int(head_dim))
 
 
 def _host_i64(values) -> np.ndarray:
@@ -590,18 +546,10 @@ def cachegen_unpack_dequantize(
     if offs.size != bits.size + 1:
         raise RuntimeError("offsets length must be bits_per_layer length + 1")
     max_key, max_value = max_key.contiguous(), max_value.contiguous()
-    max_code = _max_tensors(max_key, max_value)
-    out = torch.empty((layers, 2, int(heads), int(tokens), int(head_dim)), dtype=torch.float16,
-                      device=flat.device)
-    with _device_guard(flat.device):
-        _native.call(
-            "origami_cachegen_unpack_dequantize",
-            flat.data_ptr(), flat.numel(), _native.host_ptr(offs), _native.host_ptr(bits),
-            _native.host_ptr(kb), _native.host_ptr(vb), layers, max_key.data_ptr(),
-            max_value.data_ptr(), max_key.numel(), max_value.numel(), max_code, int(tokens),
-            int(heads), int(head_dim), out.data_ptr(), out.numel() * 2,
-            _stream_handle(flat.device))
-    return out
+    _max_tensors(max_key, max_value)
+    return _ext.ext().cachegen_unpack_dequantize_cuda(
+        flat, torch.from_numpy(offs), torch.from_numpy(bits), torch.from_numpy(kb),
+        torch.from_numpy(vb), max_key, max_value, int(tokens), int(heads), int(head_dim))
 
 
 _KIVI_PACKING = {"lsb": _native.KIVI_PACKED_LSB, "kivi": _native.KIVI_NIBBLE3}
@@ -642,125 +590,31 @@ def kivi_dequantize_to_kv_cache(
         raise RuntimeError("KIVI metadata tensors must be float16 or float32")
     if symbol_packing not in _KIVI_PACKING:
         raise ValueError(f"symbol_packing must be one of {sorted(_KIVI_PACKING)}")
-    counts = _native.i64_array([t.numel() for t in metas])
     ids = block_ids.to(device=kv_cache.device, dtype=torch.int64).contiguous()
-    code, nb, bs = dequant_cache_geometry(kv_cache, heads, head_dim)
-    with _device_guard(kv_cache.device):
-        _native.call(
-            "origami_kivi_dequantize_to_kv_cache",
-            flat.data_ptr(), flat.numel(), int(key_offset), int(key_bytes), int(value_offset),
-            int(value_bytes), int(bits), _KIVI_PACKING[symbol_packing], int(group_size),
-            int(sink_tokens), *[t.data_ptr() for t in metas], _native.host_ptr(counts),
-            _DTYPE_CODES[metas[0].dtype], kv_cache.data_ptr(), _DTYPE_CODES[kv_cache.dtype], code,
-            nb, bs, ids.data_ptr(), ids.numel(), int(tokens), int(heads), int(head_dim),
-            _stream_handle(kv_cache.device))
+    dequant_cache_geometry(kv_cache, heads, head_dim)
+    _ext.ext().kivi_dequantize_to_kv_cache(
+        flat, int(key_offset), int(key_bytes), int(value_offset), int(value_bytes), int(bits),
+        _KIVI_PACKING[symbol_packing], int(group_size), int(sink_tokens), *metas, kv_cache, ids,
+        int(tokens), int(heads), int(head_dim))
 
 
 # ---------------------------------------------------------------------------
 # Reference extension surface (origami_bitpack_cuda_v6, cpp:894-903)
 # ---------------------------------------------------------------------------
 
-class _Extension:
-    """The function names the reference extension module exports."""
-
-    @staticmethod
-    def unpack_canonical_storage_chunks_cuda(
-        flat_chunks: torch.Tensor, chunk_offsets: torch.Tensor, bits_per_chunk: torch.Tensor,
-        source_shape: torch.Tensor, axis_positions: torch.Tensor, token_count: int,
-        num_heads: int, head_dim: int, chunk_specs: torch.Tensor,
-    ) -> torch.Tensor:
-        """Signature of bitpack_layout_cuda.cpp:316-325.  Metadata tensors may
-        live on any device (host copies are taken once per call)."""
-        _require_cuda(flat_chunks, "flat_chunks")
-        shape = [int(x) for x in source_shape.reshape(-1).tolist()]
-        axes = [int(x) for x in axis_positions.reshape(-1).tolist()]
-        if len(axes) != 4:
-            raise RuntimeError(
-                "axis_positions must be [token_axis, head_axis, head_dim_axis, layer_axis]")
-        names = ["?"] * len(shape)
-        for name, pos in zip(("token", "head", "head_dim", "layer"), axes):
-            if 0 <= pos < len(names):
-                names[pos] = name
-        if "?" in names:
-            raise RuntimeError("token axis must be present in source layout")
-        offsets = np.ascontiguousarray(chunk_offsets.detach().to("cpu", torch.int64).numpy())
-        bits = [int(b) for b in bits_per_chunk.detach().to("cpu").tolist()]
-        layout = CanonicalLayout.make(shape, names, bits, chunk_specs)
-        if (layout.token_count, layout.num_heads, layout.head_dim) != (
-                int(token_count), int(num_heads), int(head_dim)):
-            raise RuntimeError("source axis sizes must match token_count/num_heads/head_dim")
-        if offsets.shape != layout.offsets.shape:
-            raise RuntimeError("chunk_offsets length must be chunk count + 1")
-        if not np.array_equal(np.diff(offsets), np.diff(layout.offsets)):
-            raise RuntimeError("Origami CUDA packed chunk byte size mismatch")
-        base = int(offsets[0]) if offsets.size else 0
-        flat = flat_chunks.reshape(-1)[base:]
-        return unpack_layout(flat, layout)
-
-    @staticmethod
-    def cachegen_unpack_dequantize_to_kv_cache_cuda(
-        bytestream: torch.Tensor, key_offset: int, key_bytes: int, value_offset: int,
-        value_bytes: int, key_bits: int, value_bits: int, key_bins: int, value_bins: int,
-        max_key: torch.Tensor, max_value: torch.Tensor, kv_cache: torch.Tensor,
-        block_ids: torch.Tensor, tokens: int, heads: int, head_dim: int,
-    ) -> None:
-        """Signature of bitpack_layout_cuda.cpp:475-491."""
-        for t, name in ((bytestream, "bytestream"), (block_ids, "block_ids")):
-            _require_cuda(t, name)
-        if block_ids.dtype != torch.int64:
-            raise RuntimeError("block_ids must be int64")
-        cachegen_unpack_dequantize_to_kv_cache(
-            bytestream, key_offset=key_offset, key_bytes=key_bytes, value_offset=value_offset,
-            value_bytes=value_bytes, key_bits=key_bits, value_bits=value_bits,
-            key_bins=key_bins, value_bins=value_bins, max_key=max_key, max_value=max_value,
-            kv_cache=kv_cache, block_ids=block_ids, tokens=tokens, heads=heads,
-            head_dim=head_dim)
-
-    @staticmethod
-    def kivi_dequantize_to_kv_cache_cuda(
-        bytestream: torch.Tensor, key_offset: int, key_bytes: int, value_offset: int,
-        value_bytes: int, bits: int, group_size: int, sink_tokens: int, key_scale: torch.Tensor,
-        key_zero: torch.Tensor, value_scale: torch.Tensor, value_zero: torch.Tensor,
-        key_sink: torch.Tensor, value_sink: torch.Tensor, kv_cache: torch.Tensor,
-        block_ids: torch.Tensor, tokens: int, heads: int, head_dim: int,
-    ) -> None:
-        """Signature of bitpack_layout_cuda.cpp:583-602 (LSB-first symbols)."""
-        for t, name in ((bytestream, "bytestream"), (block_ids, "block_ids")):
-            _require_cuda(t, name)
-        if block_ids.dtype != torch.int64:
-            raise RuntimeError("block_ids must be int64")
-        kivi_dequantize_to_kv_cache(
-            bytestream, key_offset=key_offset, key_bytes=key_bytes, value_offset=value_offset,
-            value_bytes=value_bytes, bits=bits, group_size=group_size, sink_tokens=sink_tokens,
-            key_scale=key_scale, key_zero=key_zero, value_scale=value_scale,
-            value_zero=value_zero, key_sink=key_sink, value_sink=value_sink, kv_cache=kv_cache,
-            block_ids=block_ids, tokens=tokens, heads=heads, head_dim=head_dim)
-
-    @staticmethod
-    def cachegen_unpack_dequantize_cuda(
-        bytestream: torch.Tensor, offsets: torch.Tensor, bits_per_layer: torch.Tensor,
-        key_bins: torch.Tensor, value_bins: torch.Tensor, max_key: torch.Tensor,
-        max_value: torch.Tensor, tokens: int, heads: int, head_dim: int,
-    ) -> torch.Tensor:
-        """Signature of bitpack_layout_cuda.cpp:402-412."""
-        _require_cuda(bytestream, "bytestream")
-        return cachegen_unpack_dequantize(
-            bytestream, offsets, bits_per_layer, key_bins, value_bins, max_key, max_value,
-            tokens=tokens, heads=heads, head_dim=head_dim)
-
-    @staticmethod
-    def fused_prefix_attention_cuda(*args: Any, **kwargs: Any) -> None:
-        raise NotImplementedError("fused prefix attention is outside the layout path")
-
-
 @lru_cache(maxsize=1)
-def load_bitpack_cuda_extension() -> _Extension:
+def load_bitpack_cuda_extension():
     """Counterpart of native_gpu.load_bitpack_cuda_extension (py:35-49): the
-    AOT-built HIP library instead of a JIT-built CUDA extension."""
+    AOT-built PyTorch-ROCm module origami_bitpack_hip instead of a JIT-built
+    CUDA extension.  It exports the reference module's functions
+    (unpack_canonical_storage_chunks_cuda, cachegen_unpack_dequantize_cuda,
+    cachegen_unpack_dequantize_to_kv_cache_cuda,
+    kivi_dequantize_to_kv_cache_cuda, fused_prefix_attention_cuda) with their
+    argument lists; chunk metadata may be host or device tensors (device
+    ones cost one device-to-host copy each, as in the reference)."""
     if not torch.cuda.is_available():
         raise RuntimeError("Origami HIP layout library requires a ROCm GPU")
-    _native.lib()
-    return _Extension()
+    return _ext.ext()
 
 
 __all__ = [

@@ -129,3 +129,21 @@ def test_plane_plan_flags_irregular_layouts():
     _native.call("origami_plan_planes", offs.ctypes.data, bits_a.ctypes.data, sp.ctypes.data,
                  2, 16, 1, 16, table.ctypes.data, 16, info.ctypes.data)
     assert info[1] == 0
+
+
+def test_extension_module_exports_reference_names():
+    """origami_bitpack_hip loads without a GPU and exports the reference
+    module's functions (bitpack_layout_cuda.cpp:894-903) and the fused paths."""
+    from origami_amd import _ext
+
+    m = _ext.ext()
+    for name in ("unpack_canonical_storage_chunks_cuda", "cachegen_unpack_dequantize_cuda",
+                 "cachegen_unpack_dequantize_to_kv_cache_cuda",
+                 "kivi_dequantize_to_kv_cache_cuda", "fused_prefix_attention_cuda",
+                 "unpack_canonical_to_kv_cache", "pack_canonical_from_kv_cache",
+                 "unpack_canonical_to_kv_cache_batch", "pack_canonical_storage_chunks",
+                 "kivi_dequantize_to_kv_cache"):
+        assert callable(getattr(m, name)), name
+    assert m.abi_version() == _native.ABI_VERSION
+    with pytest.raises(RuntimeError, match="outside the layout path"):
+        m.fused_prefix_attention_cuda()
