@@ -29,6 +29,8 @@ HBM_PEAK_GBPS = 8000.0
 METRIC = "KV restore GB/s (unpack+scatter) and % of HBM peak; per-layer restore µs"
 CAL_BYTES = 256 << 20
 
+CONFIG_NAMES = ("llama3-8b-4k", "qwen2.5-7b-batch", "llama3-8b-fp8-16x16k", "llama3-70b-128k")
+
 # name -> (layers, tokens); both: 8 KV heads, head_dim 128, bf16, block_size 16
 WORKLOADS = {
     "llama3-8b-32k": (32, 32768),      # Llama-3-8B geometry, one 32768-token request
@@ -65,6 +67,9 @@ def parse_args():
                     help="only the timed restore loop (for rocprofv3 runs)")
     ap.add_argument("--profile-dequant", action="store_true",
                     help="with --profile-only: also run the dequantize legs")
+    ap.add_argument("--profile-config", choices=sorted(CONFIG_NAMES), default=None,
+                    help="only the restore loop of one of the other geometries (for "
+                         "rocprofv3 runs), then the calibration copy")
     return ap.parse_args()
 
 
@@ -92,6 +97,12 @@ def main() -> int:
         return 1
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.profile_config:
+        res = configs_leg(dev, args.steps, args.config_layers, only=args.profile_config,
+                          min_launches=0)
+        calibration_copy(dev)
+        print(json.dumps(res), flush=True)
+        return 0
 
     L, T, H, D, bs, bits = (args.layers, args.tokens, args.heads, args.head_dim,
                             args.block_size, args.bits)
@@ -168,13 +179,7 @@ def main() -> int:
         if args.profile_dequant:
             dequant_leg(src_cache, T, bs, torch.zeros_like(dst_caches[0]), dst_ids[0], gen, dev,
                         args.steps)
-        # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain device
-        # copy of a known size (256 MiB read + 256 MiB written per launch)
-        cal_a = torch.empty(CAL_BYTES, dtype=torch.uint8, device=dev)
-        cal_b = torch.empty_like(cal_a)
-        for _ in range(3):
-            cal_b.copy_(cal_a)
-        torch.cuda.synchronize()
+        calibration_copy(dev)
         print(json.dumps({"ms_per_step": ms_per_step, "value_gbps": value,
                           "avg_launch_us": avg_launch_ms * 1e3,
                           "calibration_copy_bytes": CAL_BYTES}), flush=True)
@@ -245,6 +250,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": committed_traffic(args),
+            "traffic_source": ("profiles/rows_unpack_llama3_8b_32k.txt: EA read/write requests "
+                               "by size from rocprofv3 --pmc runs of bench.py --profile-only "
+                               "(not measured in this run)"),
             "kernel": "rows_unpack_kernel<8, 2> (b = 8, 16-byte aligned runs)",
             "avg_launch_us": round(avg_launch_ms * 1e3, 2),
         },
@@ -339,6 +347,19 @@ def dequant_leg(src_cache, T, bs, dst_cache, dst_ids, gen, dev, steps):
     return legs
 
 
+def calibration_copy(dev):
+    """A plain device copy of a known size (256 MiB read + 256 MiB written per
+    launch, three launches) at the end of a profiling run: the memory
+    counters of the same run must read these bytes for it."""
+    import torch
+
+    cal_a = torch.empty(CAL_BYTES, dtype=torch.uint8, device=dev)
+    cal_b = torch.empty_like(cal_a)
+    for _ in range(3):
+        cal_b.copy_(cal_a)
+    torch.cuda.synchronize()
+
+
 def _planner_layout(T, H, C):
     from origami_amd.layout import kv_symbol_layout
     from origami_amd.lossless.chunking import plan_head_channel_chunks
@@ -384,7 +405,7 @@ def _closed_form_ok(stream, src_tokens, cache, ids, T, H, C):
     return bool(torch.equal(got[:, :T], src_tokens)) and not bool(got[:, T:].any())
 
 
-def configs_leg(dev, steps, layers):
+def configs_leg(dev, steps, layers, only=None, min_launches=200):
     """Restore throughput at the other KV geometries, `layers` layers each
     (every layer has its own paged cache and streams):
 
@@ -487,8 +508,9 @@ def configs_leg(dev, steps, layers):
                 for (stream, lay, T, _), ids in zip(reqs, ids_dev):
                     native_gpu.unpack_to_kv_cache(stream, lay, T, cache, ids)
 
-        # at least ~200 launches per timing, so short layers reach steady state
-        passes = max(steps, -(-200 // (nlayers * (1 if batch else len(lengths)))))
+        # at least ~min_launches launches per timing, so short layers reach
+        # steady state
+        passes = max(steps, -(-min_launches // (nlayers * (1 if batch else len(lengths)))))
         ms = _time_passes(batched_pass if batch else per_request_pass, dev, passes)
         res = {
             "layers": nlayers, "requests_per_layer": len(lengths),
@@ -513,12 +535,21 @@ def configs_leg(dev, steps, layers):
         del layers_items, batches
         torch.cuda.empty_cache()
 
-    build("llama3-8b-4k", 8, 128, torch.bfloat16, [4096], 0, False, identity=True, nlayers=1)
-    lengths = np.random.default_rng(2).integers(8192, 65537, 8)
-    build("qwen2.5-7b-batch", 4, 128, torch.bfloat16, lengths, 2, True, batch=True)
-    build("llama3-8b-fp8-16x16k", 8, 128, torch.float8_e4m3fn, [16384] * 16, 3, False,
-          batch=True)
-    build("llama3-70b-128k", 8, 128, torch.bfloat16, [131072], 4, False)
+    geometries = {
+        "llama3-8b-4k": lambda: build("llama3-8b-4k", 8, 128, torch.bfloat16, [4096], 0, False,
+                                      identity=True, nlayers=1),
+        "qwen2.5-7b-batch": lambda: build(
+            "qwen2.5-7b-batch", 4, 128, torch.bfloat16,
+            np.random.default_rng(2).integers(8192, 65537, 8), 2, True, batch=True),
+        "llama3-8b-fp8-16x16k": lambda: build("llama3-8b-fp8-16x16k", 8, 128,
+                                              torch.float8_e4m3fn, [16384] * 16, 3, False,
+                                              batch=True),
+        "llama3-70b-128k": lambda: build("llama3-70b-128k", 8, 128, torch.bfloat16, [131072], 4,
+                                         False),
+    }
+    for name in CONFIG_NAMES:
+        if only is None or only == name:
+            geometries[name]()
     return out
 
 
@@ -670,12 +701,13 @@ def pipeline_leg(streams, layout, T, dst_caches, dst_ids, dev, kernel_ms):
     }
 
 
-TRAFFIC_FILE = REPO / "profiles" / "rows_unpack_llama3_8b_32k_traffic.txt"
+TRAFFIC_FILE = REPO / "profiles" / "rows_unpack_llama3_8b_32k.txt"
 
 
 def committed_traffic(args):
     """HBM bytes per launch of the restore kernel from the committed PMC
-    summary (FETCH_SIZE + WRITE_SIZE, calibrated), for the default workload."""
+    summary (size-resolved EA read and write requests of separate rocprofv3
+    --pmc runs, not of this run), for the default workload."""
     default = (args.layers, args.tokens, args.heads, args.head_dim, args.block_size,
                args.bits) == (32, 32768, 8, 128, 16, 8)
     if not default or not TRAFFIC_FILE.exists():
