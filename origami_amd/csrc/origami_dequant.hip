@@ -337,10 +337,12 @@ __global__ __launch_bounds__(kDqThreads) void cachegen_dense_generic_kernel(
 // waves along channels) is 8 * LT tokens x 128 channels; the value metadata
 // of its tokens is staged in LDS.
 
-constexpr int kKiviWavesC = 2;
-constexpr int kKiviThreads = 64 * kKiviWavesC;
-constexpr int kKiviTileChannels = 64 * kKiviWavesC;
-constexpr int kKiviMaxGroups = kKiviTileChannels / 16;  // value groups per tile (group >= 16)
+// Waves along channels per workgroup: 4 (256 channels) at widths up to 2
+// bits, else 2.  Measured on a 32768-token Llama-3-8B layer in separate
+// processes: at b = 2, 4 waves 37.0-38.4 us against 40.3-41.8 for 2; at
+// b = 3, 2 waves 42.1-42.7 against 46.2-47.2 for 4; 8 and 16 waves (whole
+// 2 KiB rows per workgroup) were slower at both widths.
+constexpr int kivi_waves_c(int sbits) { return sbits <= 2 ? 4 : 2; }
 
 // Body tokens per lane at `sbits` stored bits per symbol.  Fewer tokens per
 // lane means more waves and shorter store bursts; more means longer plane
@@ -383,7 +385,7 @@ __device__ __forceinline__ int64_t kivi_row(const KiviParams& p, int half, int64
 template <bool BF16, bool META_HALF>
 __device__ __forceinline__ void kivi_sink_rows(const KiviParams& p, int half, int64_t wg) {
   const int64_t G = p.C >> 3;
-  const int64_t i = wg * kKiviThreads + threadIdx.x;
+  const int64_t i = wg * blockDim.x + threadIdx.x;
   if (i >= p.sink * G) return;
   const int64_t t = i / G, g = i - t * G;
   const int64_t blk = t / p.bs;
@@ -401,7 +403,10 @@ __device__ __forceinline__ void kivi_sink_rows(const KiviParams& p, int half, in
 }
 
 template <int SBITS, bool NIB3, bool BF16, bool META_HALF>
-__global__ __launch_bounds__(kKiviThreads) void kivi_cache_kernel(KiviParams p) {
+__global__ __launch_bounds__(64 * kivi_waves_c(SBITS)) void kivi_cache_kernel(KiviParams p) {
+  constexpr int kKiviThreads = 64 * kivi_waves_c(SBITS);
+  constexpr int kKiviTileChannels = kKiviThreads;              // 8 channels x 8 lanes per wave
+  constexpr int kKiviMaxGroups = kKiviTileChannels / 16;       // value groups per tile (group >= 16)
   constexpr int LT = kivi_lane_tokens(SBITS);
   constexpr int NU = (LT * SBITS + 31) / 32;  // dwords holding a lane's plane run
   constexpr int CH = LT < 16 ? LT : 16;        // tokens per store chunk
@@ -631,13 +636,15 @@ int launch_cachegen_cache(const CacheGenCacheParams& p, int bits, bool bf16, boo
 template <int SBITS, bool NIB3, bool BF16, bool META_HALF>
 int launch_kivi_rows(const KiviParams& params, int64_t body, hipStream_t stream) {
   constexpr int64_t tile_t = 8 * kivi_lane_tokens(SBITS);
+  constexpr int threads = 64 * kivi_waves_c(SBITS);
   const int64_t nst = (body + tile_t - 1) / tile_t;
-  const int64_t sink_wgs = (params.sink * (params.C / 8) + kKiviThreads - 1) / kKiviThreads;
-  ORIGAMI_REQUIRE(params.nct * nst + sink_wgs <= INT32_MAX, "KIVI layer exceeds the launch grid");
+  const int64_t sink_wgs = (params.sink * (params.C / 8) + threads - 1) / threads;
   KiviParams p = params;
+  p.nct = static_cast<int32_t>((p.C + threads - 1) / threads);
+  ORIGAMI_REQUIRE(p.nct * nst + sink_wgs <= INT32_MAX, "KIVI layer exceeds the launch grid");
   p.ntiles = static_cast<int32_t>(p.nct * nst);
   const dim3 grid(static_cast<unsigned>(p.ntiles + sink_wgs), 2);
-  hipLaunchKernelGGL((kivi_cache_kernel<SBITS, NIB3, BF16, META_HALF>), grid, dim3(kKiviThreads),
+  hipLaunchKernelGGL((kivi_cache_kernel<SBITS, NIB3, BF16, META_HALF>), grid, dim3(threads),
                      0, stream, p);
   return check_launch("kivi_cache_kernel");
 }
@@ -922,7 +929,6 @@ int origami_kivi_dequantize_to_kv_cache(
 #undef ORIGAMI_KIVI_GENERIC
     return check_launch("kivi_generic_kernel");
   }
-  p.nct = static_cast<int32_t>((C + kKiviTileChannels - 1) / kKiviTileChannels);
   if (bf16) {
     return mhalf ? launch_kivi_cache<true, true>(p, body, sbits, nib3, st)
                  : launch_kivi_cache<true, false>(p, body, sbits, nib3, st);
