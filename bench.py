@@ -262,8 +262,14 @@ def main() -> int:
     }
 
     if not args.no_pipeline:
-        result["pipeline"] = pipeline_leg(streams, layout, T, dst_caches, dst_ids, dev,
+        host = [torch.empty(layout.stream_bytes, dtype=torch.uint8, pin_memory=True)
+                for _ in range(L)]
+        for h, s_ in zip(host, streams):
+            h.copy_(s_)
+        result["pipeline"] = pipeline_leg(host, layout, T, dst_caches, dst_ids, dev,
                                           avg_launch_ms)
+        del host
+        result["pipeline_llama3_70b_128k"] = pipeline_70b_leg(dev)
 
     if not args.no_dequant:
         result["dequant"] = dequant_leg(src_cache, T, bs, torch.zeros_like(dst_caches[0]),
@@ -633,20 +639,25 @@ def connector_leg(dev, layers, T, H, D, bs):
     }
 
 
-def pipeline_leg(streams, layout, T, dst_caches, dst_ids, dev, kernel_ms):
+def pipeline_leg(host, layout, T, dst_caches, dst_ids, dev, kernel_ms, layers=None):
     """Layer-wise restore from pinned host memory with the copy of layer L+1
     overlapped with the unpack+scatter of layer L, against the H2D copies
-    alone.  "exposed" is the time the restore adds on top of the copies."""
+    alone.  "exposed" is the time the restore adds on top of the copies.
+    Layer i reads host[i % len(host)] and restores into dst_caches[i % ...]
+    through dst_ids[i % ...] (a ring, so a long model needs only a few
+    buffers).  restore_ok: the last layer's cache equals a direct restore of
+    its stream."""
     import torch
 
+    from origami_amd.lossless import native_gpu
     from origami_amd.restore_pipeline import LayerRestorePipeline
 
-    L = len(streams)
+    L = layers or len(host)
     nbytes = layout.stream_bytes
-    host = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(L)]
-    for h, s in zip(host, streams):
-        h.copy_(s)
-    expect = dst_caches[L - 1].clone()
+    last = (L - 1) % len(dst_caches)
+    expect = torch.zeros_like(dst_caches[last])
+    native_gpu.unpack_to_kv_cache(host[(L - 1) % len(host)].to(dev), layout, T, expect,
+                                  dst_ids[last])
     for c in dst_caches:
         c.zero_()
     pipe = LayerRestorePipeline(dev, nbytes, num_slots=3, host_staging=False)
@@ -655,33 +666,36 @@ def pipeline_leg(streams, layout, T, dst_caches, dst_ids, dev, kernel_ms):
     def copies_only():
         start = torch.cuda.Event(enable_timing=True)
         start.record(pipe.copy_stream)
-        for h in host:
-            end = pipe.copy_only(h, nbytes)
-        last = torch.cuda.Event(enable_timing=True)
-        last.record(pipe.copy_stream)
+        for layer in range(L):
+            pipe.copy_only(host[layer % len(host)], nbytes)
+        end = torch.cuda.Event(enable_timing=True)
+        end.record(pipe.copy_stream)
         pipe.synchronize()
-        return start.elapsed_time(last)
+        return start.elapsed_time(end)
 
     def pipelined(compute=True):
         start = torch.cuda.Event(enable_timing=True)
         start.record(pipe.copy_stream)
         for layer in range(L):
+            h = host[layer % len(host)]
             if compute:
-                pipe.restore_pinned(host[layer], layout, T, dst_caches[layer], dst_ids[layer])
+                k = layer % len(dst_caches)
+                pipe.restore_pinned(h, layout, T, dst_caches[k], dst_ids[k])
             else:
-                pipe.submit(host[layer], nbytes, lambda flat: None)
-        last = torch.cuda.Event(enable_timing=True)
-        last.record(pipe.compute_stream)
+                pipe.submit(h, nbytes, lambda flat: None)
+        end = torch.cuda.Event(enable_timing=True)
+        end.record(pipe.compute_stream)
         pipe.synchronize()
-        return start.elapsed_time(last)
+        return start.elapsed_time(end)
 
+    reps = 3 if L * nbytes <= (8 << 30) else 2
     copies_only()
     pipelined()
     pipelined(False)
-    h2d = min(copies_only() for _ in range(3))
-    full = min(pipelined() for _ in range(3))
-    handoff = min(pipelined(False) for _ in range(3))
-    ok = bool(torch.equal(dst_caches[L - 1], expect))
+    h2d = min(copies_only() for _ in range(reps))
+    full = min(pipelined() for _ in range(reps))
+    handoff = min(pipelined(False) for _ in range(reps))
+    ok = bool(torch.equal(dst_caches[last], expect))
     return {
         "layers": L,
         "h2d_ms": round(h2d, 3),
@@ -697,8 +711,51 @@ def pipeline_leg(streams, layout, T, dst_caches, dst_ids, dev, kernel_ms):
         # identical pipeline without compute
         "restore_hidden": bool(full - handoff <= 2 * kernel_ms),
         "restore_ok": ok,
-        "source": "pinned host memory, 3 device slots, copy and compute streams",
+        "source": (f"pinned host memory ({len(host)} buffers of {nbytes} B), 3 device slots, "
+                   "copy and compute streams"),
     }
+
+
+def pipeline_70b_leg(dev):
+    """The Llama-3-70B geometry restored layer-wise from pinned host memory:
+    80 layers of one 131072-token request (8 KV heads, head_dim 128, bf16,
+    block size 16, 512 chunks of 1 MiB, permuted tables, seed 4), 512 MiB of
+    stream per layer.  Four distinct streams and caches form the ring (2 GiB
+    pinned, 2.5 GiB of caches), so the 40 GiB model needs no 40 GiB of host
+    memory."""
+    import torch
+
+    from origami_amd.lossless import native_gpu
+    from origami_amd.synthetic import fill_layer
+
+    T, H, D, bs, L, ring = 131072, 8, 128, 16, 80, 4
+    C = 2 * D
+    nblk = T // bs
+    NB = nblk + nblk // 4
+    layout = _planner_layout(T, H, C)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    src = torch.empty((2, NB, bs, H, D), dtype=torch.bfloat16, device=dev)
+    host, caches, ids = [], [], []
+    for _ in range(ring):
+        sid = torch.randperm(NB, generator=gen, device=dev)[:nblk].contiguous()
+        fill_layer(src, sid, gen)
+        h = torch.empty(layout.stream_bytes, dtype=torch.uint8, pin_memory=True)
+        h.copy_(native_gpu.pack_from_kv_cache(src, sid, T, layout))
+        host.append(h)
+        caches.append(torch.zeros((2, NB, bs, H, D), dtype=torch.bfloat16, device=dev))
+        ids.append(torch.randperm(NB, generator=gen, device=dev)[:nblk].contiguous())
+    del src
+    flat = host[0].to(dev)
+    kernel_ms = _time_passes(
+        lambda: native_gpu.unpack_to_kv_cache(flat, layout, T, caches[0], ids[0]), dev, 8)
+    del flat
+    torch.cuda.empty_cache()
+    res = pipeline_leg(host, layout, T, caches, ids, dev, kernel_ms, layers=L)
+    res["per_layer_restore_us"] = round(kernel_ms * 1e3, 2)
+    del host, caches
+    torch.cuda.empty_cache()
+    return res
 
 
 TRAFFIC_FILE = REPO / "profiles" / "rows_unpack_llama3_8b_32k.txt"

@@ -29,7 +29,8 @@ request that needs a larger slot replaces the device's pipeline; the old one
 stays referenced until no caller holds a lease on it and its last queued
 work has completed.
 
-All streams are created at the default priority.
+Pipelines on one device share one copy and one compute stream (created once
+per process); all streams are created at the default priority.
 """
 from __future__ import annotations
 
@@ -90,6 +91,26 @@ class _StagingPool:
             self._cond.notify()
 
 
+_stream_lock = threading.Lock()
+_side_streams: dict[int, tuple[torch.cuda.Stream, torch.cuda.Stream]] = {}
+
+
+def side_streams(device: torch.device) -> tuple[torch.cuda.Stream, torch.cuda.Stream]:
+    """The (copy, compute) stream pair of `device`, created once per process.
+    Every pipeline on the device uses the same pair: streams share the
+    process's few hardware queues, and a new pair per pipeline could land
+    copy and compute on one queue, which serialises them (measured: one of
+    six pipelines created in a row lost the overlap entirely)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    with _stream_lock:
+        pair = _side_streams.get(index)
+        if pair is None:
+            dev = torch.device("cuda", index)
+            pair = (torch.cuda.Stream(dev), torch.cuda.Stream(dev))
+            _side_streams[index] = pair
+        return pair
+
+
 class LayerRestorePipeline:
     """Copy/compute-overlapped restore of one layer at a time into a cache."""
 
@@ -102,8 +123,7 @@ class LayerRestorePipeline:
         if self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
         self.slot_bytes = int(slot_bytes)
-        self.copy_stream = torch.cuda.Stream(self.device)
-        self.compute_stream = torch.cuda.Stream(self.device)
+        self.copy_stream, self.compute_stream = side_streams(self.device)
         self._slots: list[_Slot] = []
         for _ in range(max(2, int(num_slots))):
             dev = torch.empty(self.slot_bytes, dtype=torch.uint8, device=self.device)
