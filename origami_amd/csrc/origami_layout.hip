@@ -398,6 +398,15 @@ constexpr int kThreads = 256;          // generic and block-copy kernels
 // bandwidth, so idle CUs cost more than short runs.
 constexpr int kRowsMaxWaves = 16;
 constexpr int kRowsThreads = kRowsMaxWaves * 64;  // launch bound
+// A restore launch with at least kRowsSplitTiles tiles per CU dispatches each
+// tile as waves / kRowsSplitWaves workgroups of kRowsSplitWaves waves, each a
+// column of wave tiles along tokens (same tile geometry and order).  Per layer:
+// 70B layer (8 tiles per CU) 233.9 -> 224.0 us against whole-tile workgroups.
+// Launches of 2 tiles per CU stay whole-tile: the 32768-token layer ran 53.7 us
+// whole against 58.4 us in 4-wave slices (8-wave slices: 59.7 us), and batched
+// restores gained nothing.
+constexpr int kRowsSplitWaves = 4;
+constexpr int kRowsSplitTiles = 4;
 constexpr int kSegTokens = 16;         // tokens per lane
 constexpr int kLaneSegs = 8;           // lanes along tokens in a wave tile
 constexpr int kLaneGroups = 8;         // lanes along 16-channel groups
@@ -710,8 +719,12 @@ struct TileCoord {
   int64_t t0;
 };
 
-// Tile order: token tiles fastest, then channel tiles, heads, halves.
-__device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, int64_t tile) {
+// Tile order: token tiles fastest, then channel tiles, heads, halves.  Inside a
+// tile, whole-tile workgroups order wave tiles along channels fastest; with
+// SPLIT, workgroup `slice` holds waves [4 slice, 4 slice + 4) and wave tiles
+// run along tokens fastest, so a workgroup is one channel column of the tile.
+template <bool SPLIT = false>
+__device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, int64_t tile, int slice = 0) {
   const int st = static_cast<int>(tile % p.nst);
   tile /= p.nst;
   const int qt = static_cast<int>(tile % p.nqt);
@@ -719,8 +732,17 @@ __device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, int64_t til
   TileCoord tc;
   tc.h = static_cast<int>(tile % p.H);
   tc.half = static_cast<int>(tile / p.H);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wqi = wave % p.wq, wsi = wave / p.wq;
+  const int lane = threadIdx.x & 63;
+  int wqi, wsi;
+  if constexpr (SPLIT) {
+    const int wave = slice * kRowsSplitWaves + (threadIdx.x >> 6);
+    wqi = wave / p.ws;
+    wsi = wave % p.ws;
+  } else {
+    const int wave = threadIdx.x >> 6;
+    wqi = wave % p.wq;
+    wsi = wave / p.wq;
+  }
   tc.slot = wqi * kLaneGroups + (lane >> 3);
   tc.q = qt * p.wq * kLaneGroups + tc.slot;
   tc.t0 = p.token0 + (static_cast<int64_t>(st * p.ws + wsi) * kLaneSegs + (lane & 7)) * kSegTokens;
@@ -782,10 +804,10 @@ __device__ __forceinline__ int64_t cursor_row(const RowsParams& p, int half, con
 // Rows kernels
 // ---------------------------------------------------------------------------
 
-template <int BITS, int MODE>
+template <int BITS, int MODE, bool SPLIT = false>
 __device__ __forceinline__ void unpack_tile(const RowsParams& p, int64_t tile,
-                                            const int64_t* desc) {
-  const TileCoord tc = tile_coord(p, tile);
+                                            const int64_t* desc, int slice = 0) {
+  const TileCoord tc = tile_coord<SPLIT>(p, tile, slice);
   if (tc.q >= p.nq || tc.t0 >= p.row_tokens) return;
   const int64_t nv = p.T - tc.t0;  // tokens of this segment that hold symbols
   const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
@@ -838,6 +860,20 @@ __global__ __launch_bounds__(kRowsThreads) void rows_unpack_kernel(RowsParams p)
   for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     load_descriptors(p, tile, desc);
     unpack_tile<BITS, MODE>(p, tile, desc);
+  }
+}
+
+// The same restore with each tile dispatched as 2^sh workgroups of
+// kRowsSplitWaves waves (p.waves = kRowsSplitWaves << sh).
+template <int BITS, int MODE>
+__global__ __launch_bounds__(kRowsSplitWaves * 64) void rows_unpack_split_kernel(RowsParams p,
+                                                                                 int sh) {
+  __shared__ int64_t desc[kTilePlanes];
+  const int64_t slots = p.ntiles << sh;
+  for (int64_t s = blockIdx.x; s < slots; s += gridDim.x) {
+    const int64_t tile = s >> sh;
+    load_descriptors(p, tile, desc);
+    unpack_tile<BITS, MODE, true>(p, tile, desc, static_cast<int>(s & ((1 << sh) - 1)));
   }
 }
 
@@ -1240,11 +1276,53 @@ int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack) {
   return pack ? kRowsBytes : kRowsShift;
 }
 
+// Restore launch in kRowsSplitWaves-wave workgroups, 2^sh per tile.
+int launch_rows_split(const RowsParams& p, int bits, int mode, hipStream_t stream) {
+  int sh = 0;
+  while ((kRowsSplitWaves << sh) < p.waves) ++sh;
+  int64_t blocks = p.ntiles << sh;
+  if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
+  if (blocks > INT32_MAX) blocks = INT32_MAX;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(64 * kRowsSplitWaves);
+  if (bits == 8 && mode == kRowsAligned16) {
+    hipLaunchKernelGGL((rows_unpack_split_kernel<8, kRowsAligned16>), grid, block, 0, stream, p,
+                       sh);
+    return check_launch("rows_unpack_split_kernel");
+  }
+  const bool window = mode == kRowsWindow;
+#define ORIGAMI_SPLIT_CASE(B)                                                                   \
+  case B:                                                                                       \
+    if (window)                                                                                 \
+      hipLaunchKernelGGL((rows_unpack_split_kernel<B, kRowsWindow>), grid, block, 0, stream, p, \
+                         sh);                                                                   \
+    else                                                                                        \
+      hipLaunchKernelGGL((rows_unpack_split_kernel<B, kRowsShift>), grid, block, 0, stream, p,  \
+                         sh);                                                                   \
+    break;
+  switch (bits) {
+    ORIGAMI_SPLIT_CASE(1)
+    ORIGAMI_SPLIT_CASE(2)
+    ORIGAMI_SPLIT_CASE(3)
+    ORIGAMI_SPLIT_CASE(4)
+    ORIGAMI_SPLIT_CASE(5)
+    ORIGAMI_SPLIT_CASE(6)
+    ORIGAMI_SPLIT_CASE(7)
+    ORIGAMI_SPLIT_CASE(8)
+    default:
+      return fail(ORIGAMI_ERR_INVALID, "Origami CUDA bitpack supports only 1..8 bit symbols");
+  }
+#undef ORIGAMI_SPLIT_CASE
+  return check_launch("rows_unpack_split_kernel");
+}
+
 int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, int mode,
                 hipStream_t stream) {
   RowsParams p = params;
   p.ntiles = nhalf * p.H * static_cast<int64_t>(p.nqt) * p.nst;
   if (p.ntiles <= 0) return ORIGAMI_OK;
+  if (!pack && p.waves > kRowsSplitWaves &&
+      p.ntiles >= kRowsSplitTiles * static_cast<int64_t>(device_cu_count()))
+    return launch_rows_split(p, bits, mode, stream);
   int64_t blocks = p.ntiles;
   if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
   if (blocks > INT32_MAX) blocks = INT32_MAX;

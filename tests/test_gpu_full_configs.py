@@ -127,3 +127,31 @@ def test_llama3_8b_fp8_16x16k_full(cuda_device):
 
 def test_llama3_70b_131072_full(cuda_device):
     _run(cuda_device, 8, 128, torch.bfloat16, [131072], 4, False, expect_chunks=512)
+
+
+@pytest.mark.parametrize("T,bits", [(131067, 8), (131072, 4), (131072, 3), (131061, 5)])
+def test_large_single_request_split_launch(cuda_device, T, bits):
+    """One ~131072-token layer (8 heads, 256-byte head rows, 2048 tiles: the
+    restore launch that dispatches each tile as 4-wave workgroups) in the
+    shift (ragged T) and window (sub-byte widths) addressing modes, against the
+    oracle's unpack + scatter of the oracle's pack."""
+    dev, H, C = cuda_device, 8, 256
+    rng = np.random.default_rng(T + bits)
+    plan = plan_head_channel_chunks(layer_index=0, num_heads=H, head_dim=C, token_count=2 * T,
+                                    bytes_per_symbol=1, min_bytes=1 << 20,
+                                    target_bytes=1 << 20, max_bytes=1 << 20)
+    specs = [[c.layout.head_start, c.layout.head_end, c.layout.channel_start,
+              c.layout.channel_end, c.layout.token_start, c.layout.token_end] for c in plan]
+    lay = kv_symbol_layout(T, H, C, bits, specs)
+    sym = rng.integers(0, 256, 2 * T * H * C, dtype=np.uint8)
+    flat, offs = oracle.pack_canonical(sym, bits, specs, [2 * T, H, C], [0, 1, 2, -1])
+    del sym
+    nblk = -(-T // BS)
+    NB = nblk + 64
+    table = rng.permutation(NB)[:nblk].astype(np.int64)
+    dst = torch.zeros((2, NB, BS, H, C // 2), dtype=torch.bfloat16, device=dev)
+    native_gpu.unpack_to_kv_cache(torch.from_numpy(flat).to(dev), lay, T, dst,
+                                  native_gpu.block_ids_tensor(table, dev, NB))
+    expect = np.zeros((2, NB, BS, H, C), dtype=np.uint8)
+    oracle.restore_layer(flat, offs, bits, specs, T, H, C, table, expect)
+    assert np.array_equal(dst.view(torch.uint8).cpu().numpy(), expect.reshape(2, NB, BS, H, C))
