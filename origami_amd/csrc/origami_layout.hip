@@ -178,6 +178,7 @@ struct PlanInfo {
   bool byte_aligned = false; // every plane starts on a byte boundary
   bool planes_even = false;  // every plane starts on a 2-byte boundary
   bool planes_dword = false; // every plane starts on a 4-byte boundary
+  bool lines128 = false;     // every plane starts on a 128-byte line (b = 8)
   // Every plane p = h * C + c is covered and starts at bit dense_base + p * T *
   // bits: the plane table is a closed form (what the chunk planner produces),
   // so the row kernels compute descriptors instead of reading a table.
@@ -200,6 +201,7 @@ PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
   info.byte_aligned = true;
   info.planes_even = true;
   info.planes_dword = true;
+  info.lines128 = true;
   for (int64_t k = 0; k < n; ++k) {
     const int64_t* s = specs + 6 * k;
     if (bits[k] != info.bits) info.bits = 0;
@@ -216,6 +218,7 @@ PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
         if (slot != -1) info.regular = false;
         slot = bit_off;
         if (bit_off % 128 != 0) info.aligned16 = false;
+        if (bit_off % 1024 != 0) info.lines128 = false;
         if (bit_off % 8 != 0) info.byte_aligned = false;
         if (bit_off % 16 != 0) info.planes_even = false;
         if (bit_off % 32 != 0) info.planes_dword = false;
@@ -223,8 +226,10 @@ PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
     }
   }
   if (info.bits != 8) info.aligned16 = false;
+  if (!info.aligned16) info.lines128 = false;
   if (!info.regular) {
     info.aligned16 = false;
+    info.lines128 = false;
     info.byte_aligned = false;
     info.planes_even = false;
     info.planes_dword = false;
@@ -428,6 +433,12 @@ enum RowsMode : int {
   kRowsAligned16 = 2,  // b = 8 and runs start on 16-byte boundaries
   kRowsShift = 3,      // unpack: runs start at any bit, any token count
   kRowsBytes = 4,      // pack: runs start on bytes, any token count
+  // b = 8, runs on 16-byte boundaries but not all on 128-byte lines: the
+  // 128 bytes that 8 lanes read or write then span two lines, each shared
+  // with the neighbouring wave, so the stream goes through the L2 normally
+  // (non-temporal loads here ran a 32784-token layer in 71.7 us, cached
+  // ones in 64.1 us; on 128-byte lines non-temporal is faster: 53.8 vs 56.3).
+  kRowsAligned16Cached = 5,
 };
 
 struct RowsParams {
@@ -456,6 +467,7 @@ struct RowsParams {
   int32_t nqt;               // workgroups along channels
   int32_t nst;               // workgroups along tokens
   int64_t ntiles;            // workgroup tiles; a workgroup loops over tiles
+  int32_t partial_last;      // the last token tile is partial: order those tiles last
   int64_t token0;            // first destination token of the tiles (a multiple of 16)
 };
 
@@ -571,10 +583,11 @@ __device__ __forceinline__ void load_run_dwords(const uint8_t* src, uint32_t* w)
 template <int BITS, int MODE>
 __device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
                                                uint32_t (&out)[4]) {
-  if constexpr (MODE == kRowsAligned16) {
+  if constexpr (MODE == kRowsAligned16 || MODE == kRowsAligned16Cached) {
     static_assert(BITS == 8, "aligned loads are for 8-bit symbols");
-    // the stream is read once: non-temporal
-    const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.stream + (P >> 3)));
+    // the stream is read once: non-temporal when each 8-lane run is one line
+    const u32x4* src = reinterpret_cast<const u32x4*>(p.stream + (P >> 3));
+    const u32x4 x = MODE == kRowsAligned16 ? __builtin_nontemporal_load(src) : *src;
     out[0] = x.x;
     out[1] = x.y;
     out[2] = x.z;
@@ -640,6 +653,8 @@ __device__ __forceinline__ void store_stream(uint8_t* dst, const uint32_t* u, in
   if constexpr (MODE == kRowsAligned16) {
     const u32x4 x = {u[0], u[1], u[2], u[3]};
     __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dst));
+  } else if constexpr (MODE == kRowsAligned16Cached) {
+    *reinterpret_cast<u32x4*>(dst) = u32x4{u[0], u[1], u[2], u[3]};
   } else if constexpr (MODE == kRowsWindow && BITS % 2 == 0) {
     if constexpr (NU == 1) {
       ORIGAMI_RUN_STORE(uint32_t, u[0], dst);
@@ -719,14 +734,36 @@ struct TileCoord {
   int64_t t0;
 };
 
-// Tile order: token tiles fastest, then channel tiles, heads, halves.  Inside a
-// tile, whole-tile workgroups order wave tiles along channels fastest; with
-// SPLIT, workgroup `slice` holds waves [4 slice, 4 slice + 4) and wave tiles
-// run along tokens fastest, so a workgroup is one channel column of the tile.
-template <bool SPLIT = false>
-__device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, int64_t tile, int slice = 0) {
+// Tile order: token tiles fastest, then channel tiles, heads, halves; when the
+// last token tile is partial, the full token tiles of every (channel tile,
+// head, half) come first and the partial ones after them, so that the small
+// tiles finish the launch instead of unbalancing its full rounds.
+// tile_token_index splits a tile index into its token tile and the rest
+// (channel tile fastest, then head, then half).
+__device__ __forceinline__ int tile_token_index(const RowsParams& p, int64_t& tile) {
+  if (p.partial_last) {
+    const int full = p.nst - 1;
+    const int64_t nfull = p.ntiles / p.nst * full;
+    if (tile >= nfull) {
+      tile -= nfull;
+      return full;
+    }
+    const int st = static_cast<int>(tile % full);
+    tile /= full;
+    return st;
+  }
   const int st = static_cast<int>(tile % p.nst);
   tile /= p.nst;
+  return st;
+}
+
+// Inside a tile, whole-tile workgroups order wave tiles along channels
+// fastest; with SPLIT, workgroup `slice` holds waves [4 slice, 4 slice + 4)
+// and wave tiles run along tokens fastest, so a workgroup is one channel
+// column of the tile.
+template <bool SPLIT = false>
+__device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, int64_t tile, int slice = 0) {
+  const int st = tile_token_index(p, tile);
   const int qt = static_cast<int>(tile % p.nqt);
   tile /= p.nqt;
   TileCoord tc;
@@ -754,8 +791,9 @@ __device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, int64_t til
 // is still reading.
 __device__ __forceinline__ void load_descriptors(const RowsParams& p, int64_t tile,
                                                  int64_t* desc) {
-  const int qt = static_cast<int>((tile / p.nst) % p.nqt);
-  const int h = static_cast<int>((tile / p.nst / p.nqt) % p.H);
+  tile_token_index(p, tile);
+  const int qt = static_cast<int>(tile % p.nqt);
+  const int h = static_cast<int>((tile / p.nqt) % p.H);
   const int n = p.wq * kWavePlanes;
   __syncthreads();
   for (int i = static_cast<int>(threadIdx.x); i < n; i += static_cast<int>(blockDim.x)) {
@@ -1184,7 +1222,10 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
     const int64_t segs_per_wg = static_cast<int64_t>(p.ws) * kLaneSegs;
     p.nst = static_cast<int32_t>((segs + segs_per_wg - 1) / segs_per_wg);
     const int64_t tiles = nhalf * H * static_cast<int64_t>(p.nqt) * p.nst;
-    if (tiles >= want || waves == 4) break;
+    if (tiles >= want || waves == 4) {
+      p.partial_last = p.nst > 1 && segs % segs_per_wg != 0;
+      break;
+    }
   }
 }
 
@@ -1193,6 +1234,7 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
 // each request's tile count and first tile.
 void set_batch_grid(RowsBatch& b, int64_t H, int64_t C) {
   RowsParams& p = b.common;
+  p.partial_last = 0;  // tile_coord's order is per request here
   if (H > 1 && p.head_pitch == C) {
     C *= H;
     H = 1;
@@ -1239,6 +1281,11 @@ int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream
     hipLaunchKernelGGL((rows_unpack_batch_kernel<8, kRowsAligned16>), grid, block, 0, stream, b);
     return check_launch("rows_unpack_batch_kernel");
   }
+  if (bits == 8 && mode == kRowsAligned16Cached) {
+    hipLaunchKernelGGL((rows_unpack_batch_kernel<8, kRowsAligned16Cached>), grid, block, 0, stream,
+                       b);
+    return check_launch("rows_unpack_batch_kernel");
+  }
   const bool window = mode == kRowsWindow;
 #define ORIGAMI_BATCH_CASE(B)                                                                    \
   case B:                                                                                        \
@@ -1269,7 +1316,14 @@ int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream
 // a multiple of 8, so its runs always start on bytes.
 int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack) {
   if (p.bit_bias == 0 && T % 16 == 0) {
-    if (info.aligned16 && aligned16(p.stream)) return kRowsAligned16;
+    if (info.aligned16 && aligned16(p.stream)) {
+      // Non-temporal when every plane starts on a 128-byte line and, for the
+      // restore, the V half too (T % 128 == 0).  The pack kept non-temporal
+      // stores faster with only the V half off the line: 4136 against 3794
+      // GB/s at T = 32832; with planes off the line, 2359 against 3160 at 32784.
+      const bool lines = info.lines128 && (reinterpret_cast<uintptr_t>(p.stream) & 127) == 0;
+      return lines && (pack || T % 128 == 0) ? kRowsAligned16 : kRowsAligned16Cached;
+    }
     const bool runs_ok = info.bits % 2 == 0 ? info.planes_dword : info.planes_even;
     if (runs_ok) return kRowsWindow;
   }
@@ -1287,6 +1341,11 @@ int launch_rows_split(const RowsParams& p, int bits, int mode, hipStream_t strea
   if (bits == 8 && mode == kRowsAligned16) {
     hipLaunchKernelGGL((rows_unpack_split_kernel<8, kRowsAligned16>), grid, block, 0, stream, p,
                        sh);
+    return check_launch("rows_unpack_split_kernel");
+  }
+  if (bits == 8 && mode == kRowsAligned16Cached) {
+    hipLaunchKernelGGL((rows_unpack_split_kernel<8, kRowsAligned16Cached>), grid, block, 0,
+                       stream, p, sh);
     return check_launch("rows_unpack_split_kernel");
   }
   const bool window = mode == kRowsWindow;
@@ -1320,6 +1379,9 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
   RowsParams p = params;
   p.ntiles = nhalf * p.H * static_cast<int64_t>(p.nqt) * p.nst;
   if (p.ntiles <= 0) return ORIGAMI_OK;
+  // partial token tiles last: restore 32784 tokens 64.0 -> 61.4 us, 49216
+  // tokens 96.8 -> 94.8 us; the pack ran 2-5% slower that way
+  if (pack) p.partial_last = 0;
   if (!pack && p.waves > kRowsSplitWaves &&
       p.ntiles >= kRowsSplitTiles * static_cast<int64_t>(device_cu_count()))
     return launch_rows_split(p, bits, mode, stream);
@@ -1332,6 +1394,13 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
       hipLaunchKernelGGL((rows_pack_kernel<8, kRowsAligned16>), grid, block, 0, stream, p);
     else
       hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsAligned16>), grid, block, 0, stream, p);
+    return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
+  }
+  if (bits == 8 && mode == kRowsAligned16Cached) {
+    if (pack)
+      hipLaunchKernelGGL((rows_pack_kernel<8, kRowsAligned16Cached>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsAligned16Cached>), grid, block, 0, stream, p);
     return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
   }
   const bool window = mode == kRowsWindow;
@@ -1452,6 +1521,7 @@ PlanInfo analyze_plan(const int64_t* offsets, const int64_t* bits, const int64_t
   info.regular = n > 0;
   info.bits = n > 0 ? static_cast<int>(bits[0]) : 0;
   info.aligned16 = info.byte_aligned = info.planes_even = info.planes_dword = true;
+  info.lines128 = true;
   bool in_order = true;  // chunk k holds planes [next, next + planes_k) in h * C + c order
   int64_t next = 0;
   for (int64_t k = 0; k < n; ++k) {
@@ -1465,6 +1535,7 @@ PlanInfo analyze_plan(const int64_t* offsets, const int64_t* bits, const int64_t
     const int64_t first = offsets[k] * 8, step = T * bits[k];
     auto all_multiple = [&](int64_t m) { return first % m == 0 && (planes == 1 || step % m == 0); };
     if (!all_multiple(128)) info.aligned16 = false;
+    if (!all_multiple(1024)) info.lines128 = false;
     if (!all_multiple(8)) info.byte_aligned = false;
     if (!all_multiple(16)) info.planes_even = false;
     if (!all_multiple(32)) info.planes_dword = false;
@@ -1488,8 +1559,10 @@ PlanInfo analyze_plan(const int64_t* offsets, const int64_t* bits, const int64_t
     }
   }
   if (info.bits != 8) info.aligned16 = false;
+  if (!info.aligned16) info.lines128 = false;
   if (!info.regular) {
     info.aligned16 = info.byte_aligned = info.planes_even = info.planes_dword = false;
+    info.lines128 = false;
   }
   if (info.regular && info.bits != 0 && in_order && next == H * C && H * C > 0) {
     info.dense = true;
