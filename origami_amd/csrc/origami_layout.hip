@@ -481,14 +481,18 @@ struct RowsRequest {
   const int64_t* block_ids;
   int64_t T, row_tokens;
   int64_t token0;  // tokens [token0, row_tokens) are restored
-  int64_t tile0;   // first workgroup tile of the request
+  int64_t tile0;   // first full-token-tile workgroup tile of the request
+  int64_t ptile0;  // first partial-token-tile workgroup tile of the request
   int32_t nst;
+  int32_t partial;  // 1: the last token tile is partial
+  int32_t nt;       // aligned16 batches: 1 = non-temporal loads (runs on 128-byte lines)
 };
 
 constexpr int kBatchRequests = 16;  // requests per batched launch (kernel arguments)
 
 struct RowsBatch {
   RowsParams common;
+  int64_t nfull;  // tiles [0, nfull) are full token tiles
   int32_t nreq;
   RowsRequest req[kBatchRequests];
 };
@@ -738,23 +742,22 @@ struct TileCoord {
 // last token tile is partial, the full token tiles of every (channel tile,
 // head, half) come first and the partial ones after them, so that the small
 // tiles finish the launch instead of unbalancing its full rounds.
-// tile_token_index splits a tile index into its token tile and the rest
-// (channel tile fastest, then head, then half).
-__device__ __forceinline__ int tile_token_index(const RowsParams& p, int64_t& tile) {
+// A tile is its token tile `st` and the rest (channel tile fastest, then
+// head, then half).
+struct TileIndex {
+  int st;
+  int64_t rest;
+};
+
+// Splits a tile index of a single-request launch.
+__device__ __forceinline__ TileIndex split_tile(const RowsParams& p, int64_t tile) {
   if (p.partial_last) {
     const int full = p.nst - 1;
     const int64_t nfull = p.ntiles / p.nst * full;
-    if (tile >= nfull) {
-      tile -= nfull;
-      return full;
-    }
-    const int st = static_cast<int>(tile % full);
-    tile /= full;
-    return st;
+    if (tile >= nfull) return {full, tile - nfull};
+    return {static_cast<int>(tile % full), tile / full};
   }
-  const int st = static_cast<int>(tile % p.nst);
-  tile /= p.nst;
-  return st;
+  return {static_cast<int>(tile % p.nst), tile / p.nst};
 }
 
 // Inside a tile, whole-tile workgroups order wave tiles along channels
@@ -762,8 +765,10 @@ __device__ __forceinline__ int tile_token_index(const RowsParams& p, int64_t& ti
 // and wave tiles run along tokens fastest, so a workgroup is one channel
 // column of the tile.
 template <bool SPLIT = false>
-__device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, int64_t tile, int slice = 0) {
-  const int st = tile_token_index(p, tile);
+__device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, TileIndex ti,
+                                                int slice = 0) {
+  const int st = ti.st;
+  int64_t tile = ti.rest;
   const int qt = static_cast<int>(tile % p.nqt);
   tile /= p.nqt;
   TileCoord tc;
@@ -789,11 +794,10 @@ __device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, int64_t til
 // Stages the tile's plane descriptors in LDS.  The leading barrier keeps a
 // workgroup that loops over tiles from overwriting descriptors another wave
 // is still reading.
-__device__ __forceinline__ void load_descriptors(const RowsParams& p, int64_t tile,
+__device__ __forceinline__ void load_descriptors(const RowsParams& p, TileIndex ti,
                                                  int64_t* desc) {
-  tile_token_index(p, tile);
-  const int qt = static_cast<int>(tile % p.nqt);
-  const int h = static_cast<int>((tile / p.nqt) % p.H);
+  const int qt = static_cast<int>(ti.rest % p.nqt);
+  const int h = static_cast<int>((ti.rest / p.nqt) % p.H);
   const int n = p.wq * kWavePlanes;
   __syncthreads();
   for (int i = static_cast<int>(threadIdx.x); i < n; i += static_cast<int>(blockDim.x)) {
@@ -843,9 +847,9 @@ __device__ __forceinline__ int64_t cursor_row(const RowsParams& p, int half, con
 // ---------------------------------------------------------------------------
 
 template <int BITS, int MODE, bool SPLIT = false>
-__device__ __forceinline__ void unpack_tile(const RowsParams& p, int64_t tile,
+__device__ __forceinline__ void unpack_tile(const RowsParams& p, TileIndex ti,
                                             const int64_t* desc, int slice = 0) {
-  const TileCoord tc = tile_coord<SPLIT>(p, tile, slice);
+  const TileCoord tc = tile_coord<SPLIT>(p, ti, slice);
   if (tc.q >= p.nq || tc.t0 >= p.row_tokens) return;
   const int64_t nv = p.T - tc.t0;  // tokens of this segment that hold symbols
   const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
@@ -896,8 +900,9 @@ template <int BITS, int MODE>
 __global__ __launch_bounds__(kRowsThreads) void rows_unpack_kernel(RowsParams p) {
   __shared__ int64_t desc[kTilePlanes];
   for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
-    load_descriptors(p, tile, desc);
-    unpack_tile<BITS, MODE>(p, tile, desc);
+    const TileIndex ti = split_tile(p, tile);
+    load_descriptors(p, ti, desc);
+    unpack_tile<BITS, MODE>(p, ti, desc);
   }
 }
 
@@ -910,19 +915,32 @@ __global__ __launch_bounds__(kRowsSplitWaves * 64) void rows_unpack_split_kernel
   const int64_t slots = p.ntiles << sh;
   for (int64_t s = blockIdx.x; s < slots; s += gridDim.x) {
     const int64_t tile = s >> sh;
-    load_descriptors(p, tile, desc);
-    unpack_tile<BITS, MODE, true>(p, tile, desc, static_cast<int>(s & ((1 << sh) - 1)));
+    const TileIndex ti = split_tile(p, tile);
+    load_descriptors(p, ti, desc);
+    unpack_tile<BITS, MODE, true>(p, ti, desc, static_cast<int>(s & ((1 << sh) - 1)));
   }
 }
 
-// One layer of several requests: the workgroup's tile range picks the
-// request (a uniform scan of at most kBatchRequests tile offsets).
+// One layer of several requests.  The full token tiles of all requests come
+// first (request by request), then every request's partial last token tile;
+// the workgroup's tile picks its request with a uniform scan of at most
+// kBatchRequests tile offsets (a request with no tiles in a range has the next
+// request's offset, so the scan passes it).
 template <int BITS, int MODE>
 __global__ __launch_bounds__(kRowsThreads) void rows_unpack_batch_kernel(RowsBatch b) {
   __shared__ int64_t desc[kTilePlanes];
   for (int64_t tile = blockIdx.x; tile < b.common.ntiles; tile += gridDim.x) {
     int r = 0;
-    while (r + 1 < b.nreq && tile >= b.req[r + 1].tile0) ++r;
+    TileIndex ti;
+    if (tile < b.nfull) {
+      while (r + 1 < b.nreq && tile >= b.req[r + 1].tile0) ++r;
+      const int full = b.req[r].nst - b.req[r].partial;
+      const int64_t local = tile - b.req[r].tile0;
+      ti = {static_cast<int>(local % full), local / full};
+    } else {
+      while (r + 1 < b.nreq && tile >= b.req[r + 1].ptile0) ++r;
+      ti = {b.req[r].nst - 1, tile - b.req[r].ptile0};
+    }
     const RowsRequest& q = b.req[r];
     RowsParams p = b.common;
     p.stream = q.stream;
@@ -936,15 +954,23 @@ __global__ __launch_bounds__(kRowsThreads) void rows_unpack_batch_kernel(RowsBat
     p.row_tokens = q.row_tokens;
     p.nst = q.nst;
     p.token0 = q.token0;
-    const int64_t local = tile - q.tile0;
-    load_descriptors(p, local, desc);
-    unpack_tile<BITS, MODE>(p, local, desc);
+    load_descriptors(p, ti, desc);
+    if constexpr (MODE == kRowsAligned16) {
+      // one launch for the batch, the load policy per request
+      if (q.nt)
+        unpack_tile<BITS, kRowsAligned16>(p, ti, desc);
+      else
+        unpack_tile<BITS, kRowsAligned16Cached>(p, ti, desc);
+    } else {
+      unpack_tile<BITS, MODE>(p, ti, desc);
+    }
   }
 }
 
 template <int BITS, int MODE>
-__device__ __forceinline__ void pack_tile(const RowsParams& p, int64_t tile, const int64_t* desc) {
-  const TileCoord tc = tile_coord(p, tile);
+__device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
+                                          const int64_t* desc) {
+  const TileCoord tc = tile_coord(p, ti);
   if (tc.q >= p.nq || tc.t0 >= p.T) return;
   const int nv = static_cast<int>(p.T - tc.t0 < 16 ? p.T - tc.t0 : 16);
 
@@ -989,8 +1015,9 @@ template <int BITS, int MODE>
 __global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
   __shared__ int64_t desc[kTilePlanes];
   for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
-    load_descriptors(p, tile, desc);
-    pack_tile<BITS, MODE>(p, tile, desc);
+    const TileIndex ti = split_tile(p, tile);
+    load_descriptors(p, ti, desc);
+    pack_tile<BITS, MODE>(p, ti, desc);
   }
 }
 
@@ -1262,11 +1289,20 @@ void set_batch_grid(RowsBatch& b, int64_t H, int64_t C) {
       tiles += 2 * H * p.nqt * nst_of(b.req[r].row_tokens - b.req[r].token0);
     if (tiles >= want || waves == 4) break;
   }
+  const int64_t per = 2 * H * static_cast<int64_t>(p.nqt);  // tiles per token tile
+  const int64_t tile_tokens = static_cast<int64_t>(p.ws) * kLaneSegs * kSegTokens;
   int64_t tile0 = 0;
   for (int r = 0; r < b.nreq; ++r) {
-    b.req[r].nst = static_cast<int32_t>(nst_of(b.req[r].row_tokens - b.req[r].token0));
+    const int64_t n = b.req[r].row_tokens - b.req[r].token0;
+    b.req[r].nst = static_cast<int32_t>(nst_of(n));
+    b.req[r].partial = n % tile_tokens != 0 ? 1 : 0;
     b.req[r].tile0 = tile0;
-    tile0 += 2 * H * p.nqt * static_cast<int64_t>(b.req[r].nst);
+    tile0 += per * (b.req[r].nst - b.req[r].partial);
+  }
+  b.nfull = tile0;
+  for (int r = 0; r < b.nreq; ++r) {
+    b.req[r].ptile0 = tile0;
+    tile0 += per * b.req[r].partial;
   }
   p.ntiles = tile0;
 }
@@ -1279,11 +1315,6 @@ int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream
   const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(64 * b.common.waves));
   if (bits == 8 && mode == kRowsAligned16) {
     hipLaunchKernelGGL((rows_unpack_batch_kernel<8, kRowsAligned16>), grid, block, 0, stream, b);
-    return check_launch("rows_unpack_batch_kernel");
-  }
-  if (bits == 8 && mode == kRowsAligned16Cached) {
-    hipLaunchKernelGGL((rows_unpack_batch_kernel<8, kRowsAligned16Cached>), grid, block, 0, stream,
-                       b);
     return check_launch("rows_unpack_batch_kernel");
   }
   const bool window = mode == kRowsWindow;
@@ -1314,7 +1345,8 @@ int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream
 // symbol count per half (a multiple of 16 keeps every lane run inside its
 // plane).  The rows pack is only launched for byte-aligned planes with T * b
 // a multiple of 8, so its runs always start on bytes.
-int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack) {
+int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack,
+              int64_t token0 = 0) {
   if (p.bit_bias == 0 && T % 16 == 0) {
     if (info.aligned16 && aligned16(p.stream)) {
       // Non-temporal when every plane starts on a 128-byte line and, for the
@@ -1322,7 +1354,10 @@ int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack) {
       // stores faster with only the V half off the line: 4136 against 3794
       // GB/s at T = 32832; with planes off the line, 2359 against 3160 at 32784.
       const bool lines = info.lines128 && (reinterpret_cast<uintptr_t>(p.stream) & 127) == 0;
-      return lines && (pack || T % 128 == 0) ? kRowsAligned16 : kRowsAligned16Cached;
+      // Lane runs start at token0 + 16 k: a batched request restored past
+      // its shared prefix needs token0 % 128 == 0 too.
+      return lines && (pack || (T % 128 == 0 && token0 % 128 == 0)) ? kRowsAligned16
+                                                                    : kRowsAligned16Cached;
     }
     const bool runs_ok = info.bits % 2 == 0 ? info.planes_dword : info.planes_even;
     if (runs_ok) return kRowsWindow;
@@ -1908,7 +1943,10 @@ int origami_unpack_canonical_to_kv_cache_batch(
                     "first_tokens must be a multiple of the block size and of 16");
     it.q.token0 = first;
     it.bits = plan->info.bits;
-    it.mode = rows_mode(plan->info, p, tokens[r], false);
+    it.mode = rows_mode(plan->info, p, tokens[r], false, first);
+    // both aligned16 policies share a launch; the kernel picks per request
+    it.q.nt = it.mode == kRowsAligned16;
+    if (it.mode == kRowsAligned16Cached) it.mode = kRowsAligned16;
     items.push_back(it);
   }
   // one launch per (width, addressing mode) group of up to kBatchRequests

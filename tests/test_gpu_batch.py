@@ -1,5 +1,6 @@
 """Batched fused restore (one layer of several requests, one launch per symbol
-width and addressing mode): byte for byte the result of restoring the
+width and addressing mode; 8-bit requests with and without 128-byte-line runs
+share a launch): byte for byte the result of restoring the
 requests one after another, and of the oracle's unpack + scatter in the same
 order, across ragged and aligned lengths, widths, more requests than one
 launch holds, both cache layouts, block sizes, shared prefix blocks (written
@@ -118,3 +119,13 @@ def test_batch_interior_shared_block(cuda_device, dedup):
 def test_batch_fp8_sized_rows(cuda_device):
     rng = np.random.default_rng(12)
     _run(cuda_device, rng, [2048] * 16, 8, 128, 8, 16, False, 0.0, False)
+
+
+@pytest.mark.parametrize("dedup", [False, True])
+def test_batch_mixed_load_policies(cuda_device, dedup):
+    """8-bit requests in one launch, some with every lane run on a 128-byte
+    line (T and the first restored token multiples of 128: non-temporal loads)
+    and some off the lines (cached loads)."""
+    rng = np.random.default_rng(77)
+    _run(cuda_device, rng, [1024, 1088, 2048, 1040, 1536, 1152], 8, 256, 8, 16, False, 0.5,
+         dedup)
