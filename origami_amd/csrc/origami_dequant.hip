@@ -116,6 +116,25 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
+// Eight binary32 values rounded and packed into four dwords (pairs low,
+// high).  One empty asm over all eight keeps the rounding barrier of
+// out_bits2 without tying each conversion to the two fma results just
+// before it (which made the compiler pad every pair with wait states).
+template <bool BF16>
+__device__ __forceinline__ void out_bits8(float (&v)[8], uint32_t (&o)[4]) {
+  asm("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]),
+      "+v"(v[7]));
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const f32x2 x = {v[2 * k], v[2 * k + 1]};
+    if constexpr (BF16) {
+      o[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2));
+    } else {
+      o[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, f16x2));
+    }
+  }
+}
+
 template <bool BF16>
 __device__ __forceinline__ uint32_t out_bits2(float a, float b) {
   asm("" : "+v"(a), "+v"(b));
@@ -402,24 +421,32 @@ __device__ __forceinline__ void kivi_sink_rows(const KiviParams& p, int half, in
   __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(p.cache + row * p.C + g * 8));
 }
 
-template <int SBITS, bool NIB3, bool BF16, bool META_HALF>
-__global__ __launch_bounds__(64 * kivi_waves_c(SBITS)) void kivi_cache_kernel(KiviParams p) {
-  constexpr int kKiviThreads = 64 * kivi_waves_c(SBITS);
-  constexpr int kKiviTileChannels = kKiviThreads;              // 8 channels x 8 lanes per wave
-  constexpr int kKiviMaxGroups = kKiviTileChannels / 16;       // value groups per tile (group >= 16)
-  constexpr int LT = kivi_lane_tokens(SBITS);
+template <int SBITS>
+struct KiviTileShape {
+  static constexpr int kThreads = 64 * kivi_waves_c(SBITS);
+  static constexpr int kChannels = kThreads;          // 8 channels x 8 lanes per wave
+  static constexpr int kMaxGroups = kChannels / 16;   // value groups per tile (group >= 16)
+  static constexpr int LT = kivi_lane_tokens(SBITS);
+  static constexpr int TILE_T = 8 * LT;
+};
+
+// One row-kernel tile of half HALF (0 keys, 1 values).  The half is a template
+// parameter so that no per-element branch on it remains in the store loop.
+template <int HALF, int SBITS, bool NIB3, bool BF16, bool META_HALF>
+__device__ __forceinline__ void kivi_tile(
+    const KiviParams& p,
+    float (&vmeta)[2][KiviTileShape<SBITS>::kMaxGroups][KiviTileShape<SBITS>::TILE_T]) {
+  using Shape = KiviTileShape<SBITS>;
+  constexpr int kKiviThreads = Shape::kThreads;
+  constexpr int kKiviTileChannels = Shape::kChannels;
+  constexpr int LT = Shape::LT;
   constexpr int NU = (LT * SBITS + 31) / 32;  // dwords holding a lane's plane run
   constexpr int CH = LT < 16 ? LT : 16;        // tokens per store chunk
-  constexpr int TILE_T = 8 * LT;
+  constexpr int TILE_T = Shape::TILE_T;
   constexpr uint32_t mask = NIB3 ? 0x7u : (1u << SBITS) - 1u;
-  __shared__ float vmeta[2][kKiviMaxGroups][TILE_T];
-  const int half = blockIdx.y;
+  constexpr int half = HALF;
   const KiviHalf& hs = p.half[half];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (static_cast<int32_t>(blockIdx.x) >= p.ntiles) {
-    kivi_sink_rows<BF16, META_HALF>(p, half, blockIdx.x - p.ntiles);
-    return;
-  }
   // Workgroups go to the 8 XCDs round-robin and each XCD has its own L2.
   // Give each XCD a contiguous range of tiles, so that the channel tiles of
   // one token range (which share their value metadata lines) and the token
@@ -435,7 +462,7 @@ __global__ __launch_bounds__(64 * kivi_waves_c(SBITS)) void kivi_cache_kernel(Ki
   // Value metadata of the tile: [scale / zero][group][token], staged once
   // (consecutive threads read consecutive groups of a token).
   const int64_t g_first = tile_c0 / p.group;
-  if (half == 1) {
+  if constexpr (HALF == 1) {
     const int64_t c_last = min(tile_c0 + kKiviTileChannels, p.C) - 1;
     const int ng = static_cast<int>(c_last / p.group - g_first + 1);
     for (int i = threadIdx.x; i < ng * TILE_T; i += kKiviThreads) {
@@ -488,7 +515,7 @@ __global__ __launch_bounds__(64 * kivi_waves_c(SBITS)) void kivi_cache_kernel(Ki
   for (int jb = 0; jb < LT / CH; ++jb) {
     if (CH * jb >= nj) break;
     float ks[8] = {}, kz[8] = {};
-    if (half == 0) {
+    if constexpr (HALF == 0) {
       const int64_t g = (bt0 + CH * jb) / p.group;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -502,39 +529,79 @@ __global__ __launch_bounds__(64 * kivi_waves_c(SBITS)) void kivi_cache_kernel(Ki
     const int jsplit = static_cast<int>(min<int64_t>(CH, p.bs - off0));
     const int64_t row_a = kivi_row(p, half, blk0, off0);
     const int64_t row_b = jsplit < nj - CH * jb ? kivi_row(p, half, blk0 + 1, 0) : -1;
-    uint16_t* const dst_a = p.cache + row_a * p.C + c0;
-    uint16_t* const dst_b = p.cache + row_b * p.C + c0;
+    // the chunk's value metadata, read before its stores
+    float vs[CH], vz[CH];
+    if constexpr (HALF == 1) {
 #pragma unroll
-    for (int jj = 0; jj < CH; ++jj) {
-      const int j = CH * jb + jj;
-      const bool second = jj >= jsplit;
-      if (j < nj && (second ? row_b : row_a) >= 0) {
-        uint32_t o[4];
+      for (int jj = 0; jj < CH; ++jj) {
+        vs[jj] = vmeta[0][gi][tt0 + CH * jb + jj];
+        vz[jj] = vmeta[1][gi][tt0 + CH * jb + jj];
+      }
+    }
+    // the 8 dequantized values of token j, as 4 packed pairs
+    auto token_bits = [&](int j, int jj, uint32_t (&o)[4]) {
+      float v[8];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          float v[2];
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int i = 2 * k + e;
-            const int bp = j * SBITS;
-            const int dw = bp >> 5, off = bp & 31;
-            uint32_t sym = u[i][dw] >> off;
-            if (off + SBITS > 32) sym |= u[i][dw + 1] << (32 - off);
-            const float s = static_cast<float>(sym & mask);
-            if (half == 0) {
-              v[e] = fma3(s, ks[i], kz[i]);
-            } else {
-              v[e] = fma3(s, vmeta[0][gi][tt0 + j], vmeta[1][gi][tt0 + j]);
-            }
-          }
-          o[k] = out_bits2<BF16>(v[0], v[1]);
+      for (int i = 0; i < 8; ++i) {
+        const int bp = j * SBITS;
+        const int dw = bp >> 5, off = bp & 31;
+        uint32_t sym = u[i][dw] >> off;
+        if (off + SBITS > 32) sym |= u[i][dw + 1] << (32 - off);
+        const float s = static_cast<float>(sym & mask);
+        if constexpr (HALF == 0) {
+          v[i] = fma3(s, ks[i], kz[i]);
+        } else {
+          v[i] = fma3(s, vs[jj], vz[jj]);
         }
-        uint16_t* dst = second ? dst_b + (jj - jsplit) * p.C : dst_a + jj * p.C;
-        const u32x4 x = {o[0], o[1], o[2], o[3]};
-        __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dst));
+      }
+      out_bits8<BF16>(v, o);
+    };
+    if (jsplit == CH) {
+      // the chunk lies in one block: one row pointer, advanced a row per token
+      if (row_a >= 0) {
+        uint16_t* dst = p.cache + row_a * p.C + c0;
+#pragma unroll
+        for (int jj = 0; jj < CH; ++jj, dst += p.C) {
+          const int j = CH * jb + jj;
+          if (j < nj) {
+            uint32_t o[4];
+            token_bits(j, jj, o);
+            const u32x4 x = {o[0], o[1], o[2], o[3]};
+            __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dst));
+          }
+        }
+      }
+    } else {
+      uint16_t* const dst_a = p.cache + row_a * p.C + c0;
+      uint16_t* const dst_b = p.cache + row_b * p.C + c0;
+#pragma unroll
+      for (int jj = 0; jj < CH; ++jj) {
+        const int j = CH * jb + jj;
+        const bool second = jj >= jsplit;
+        if (j < nj && (second ? row_b : row_a) >= 0) {
+          uint32_t o[4];
+          token_bits(j, jj, o);
+          uint16_t* dst = second ? dst_b + (jj - jsplit) * p.C : dst_a + jj * p.C;
+          const u32x4 x = {o[0], o[1], o[2], o[3]};
+          __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dst));
+        }
       }
     }
   }
+}
+
+template <int SBITS, bool NIB3, bool BF16, bool META_HALF>
+__global__ __launch_bounds__(64 * kivi_waves_c(SBITS)) void kivi_cache_kernel(KiviParams p) {
+  using Shape = KiviTileShape<SBITS>;
+  __shared__ float vmeta[2][Shape::kMaxGroups][Shape::TILE_T];
+  if (static_cast<int32_t>(blockIdx.x) >= p.ntiles) {
+    kivi_sink_rows<BF16, META_HALF>(p, blockIdx.y, blockIdx.x - p.ntiles);
+    return;
+  }
+  if (blockIdx.y == 0)
+    kivi_tile<0, SBITS, NIB3, BF16, META_HALF>(p, vmeta);
+  else
+    kivi_tile<1, SBITS, NIB3, BF16, META_HALF>(p, vmeta);
 }
 
 // One thread per destination element of both halves: any shape, any group,
