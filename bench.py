@@ -277,6 +277,7 @@ def main() -> int:
 
     if not args.no_configs:
         result["configs"] = configs_leg(dev, max(3, args.steps // 2), args.config_layers)
+        result["host_cost"] = host_cost_leg(dev)
 
     if not args.no_connector:
         result["connector"] = connector_leg(dev, args.connector_layers, T, H, D, bs)
@@ -363,6 +364,57 @@ def dequant_leg(src_cache, T, bs, dst_cache, dst_ids, gen, dev, steps, layers=4)
     del kvs, dsts
     torch.cuda.empty_cache()
     return legs
+
+
+def host_cost_leg(dev, calls=400, tokens=4096):
+    """Host time per restore call: wall time of `calls` back-to-back calls
+    of one 4096-token layer (8 KV heads, head_dim 128, bf16, bs 16, planner
+    chunks of 1 MiB) from Python, through native_gpu.unpack_to_kv_cache (the
+    full entry point: tensor checks, chunk metadata, plan lookup) and through
+    a PreparedRestore made once for the request.  The loop is timed on the host
+    from a synchronized start without waiting for the GPU; `gpu_us_per_call`
+    (events over the same calls) shows the GPU was not what limited it."""
+    import time
+
+    import torch
+
+    from origami_amd.lossless import native_gpu
+    from origami_amd.synthetic import fill_layer
+
+    H, D, bs = 8, 128, 16
+    C = 2 * D
+    nblk = -(-tokens // bs)
+    layout = _planner_layout(tokens, H, C)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(9)
+    src = torch.zeros((2, nblk, bs, H, D), dtype=torch.bfloat16, device=dev)
+    fill_layer(src, torch.arange(nblk, device=dev), gen)
+    ids = torch.arange(nblk, device=dev, dtype=torch.int64)
+    flat = native_gpu.pack_from_kv_cache(src, ids, tokens, layout)
+    cache = torch.zeros_like(src)
+    prep = native_gpu.PreparedRestore(layout, tokens, cache, ids)
+    cur = torch.cuda.current_stream(dev)
+    out = {"calls": calls, "sample": f"one {tokens}-token layer, 8 KV heads, head_dim 128, bf16"}
+    for name, fn in (("unpack_to_kv_cache", lambda: native_gpu.unpack_to_kv_cache(
+                          flat, layout, tokens, cache, ids)),
+                     ("prepared_restore", lambda: prep.restore(flat, cache))):
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        t1 = time.perf_counter()
+        e1.record(cur)
+        torch.cuda.synchronize()
+        out[f"{name}_host_us"] = round((t1 - t0) * 1e6 / calls, 2)
+        out[f"{name}_gpu_us_per_call"] = round(e0.elapsed_time(e1) * 1e3 / calls, 2)
+    ok = bool(torch.equal(cache.view(torch.uint8), src.view(torch.uint8)))
+    out["restore_ok"] = ok
+    prep.close()
+    return out
 
 
 def calibration_copy(dev):

@@ -191,6 +191,38 @@ int origami_unpack_canonical_to_kv_cache_noalloc(
     const int64_t* block_ids, int64_t block_count, origami_stream_t stream);
 
 /*
+ * Prepared fused restore: origami_unpack_canonical_to_kv_cache split into a
+ * setup done once per request (the chunk metadata validated and its plan
+ * looked up or built, a reordered plan's plane table uploaded, the cache
+ * geometry checked, the launch shape computed) and a launch per layer that
+ * takes only the layer's stream and destination cache.  It has no
+ * counterpart in the reference; it is for callers that restore every layer
+ * of a request with the same chunk plan, tokens, cache geometry and block
+ * table (the layer-wise restore of worker.py:718-1248), where the per-call
+ * host cost of the full entry point (argument checks, the plan lookup, which
+ * hashes the chunk metadata) would otherwise be paid per layer.  Results are
+ * those of origami_unpack_canonical_to_kv_cache with the same arguments.
+ * block_ids is a device array the caller keeps alive and unchanged while the
+ * plan is in use; the plan is used on the device current at creation.  The
+ * launch needs flat_bytes >= chunk_offsets[num_chunks] and a 16-byte aligned
+ * kv_cache of the geometry given at creation.  A plan may be launched from
+ * several threads; destroy it once no launch can still use it (pending
+ * kernels keep nothing of it).  create returns ORIGAMI_ERR_UNSUPPORTED where
+ * origami_unpack_canonical_to_kv_cache would.
+ */
+typedef struct origami_restore_plan* origami_restore_plan_t;
+
+int origami_restore_plan_create(
+    const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
+    const int64_t* chunk_specs, int64_t num_chunks, int64_t tokens,
+    int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+    int64_t num_heads, int64_t head_bytes, const int64_t* block_ids,
+    int64_t block_count, origami_restore_plan_t* plan);
+int origami_restore_plan_launch(origami_restore_plan_t plan, const uint8_t* flat_chunks,
+                                int64_t flat_bytes, void* kv_cache, origami_stream_t stream);
+void origami_restore_plan_destroy(origami_restore_plan_t plan);
+
+/*
  * Batched fused restore: one layer of several requests into one paged cache.
  * Request r is exactly the argument set of origami_unpack_canonical_to_kv_cache
  * (stream flat_chunks[r] of flat_bytes[r] bytes, its chunk metadata arrays,

@@ -12,7 +12,7 @@ from pathlib import Path
 import numpy as np
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liborigami_layout.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 ORIGAMI_OK = 0
 ORIGAMI_ERR_INVALID = 1
@@ -46,6 +46,9 @@ _SIGNATURES: dict[str, list] = {
         _p, _i64, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "origami_unpack_canonical_to_kv_cache_noalloc": [
         _p, _i64, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "origami_restore_plan_create": [
+        _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "origami_restore_plan_launch": [_p, _p, _i64, _p, _p],
     "origami_unpack_canonical_to_kv_cache_batch": [
         _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p],
     "origami_pack_canonical_from_kv_cache": [
@@ -62,7 +65,7 @@ _SIGNATURES: dict[str, list] = {
         _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p],
 }
 
-EXPORTED_SYMBOLS = ("origami_last_error", *_SIGNATURES)
+EXPORTED_SYMBOLS = ("origami_last_error", "origami_restore_plan_destroy", *_SIGNATURES)
 
 _lib: ctypes.CDLL | None = None
 _lock = threading.Lock()
@@ -95,6 +98,8 @@ def lib() -> ctypes.CDLL:
                 fn.restype = ctypes.c_int
                 fn.argtypes = args
             L.origami_set_rows_grid_limit.restype = ctypes.c_int64
+            L.origami_restore_plan_destroy.restype = None
+            L.origami_restore_plan_destroy.argtypes = [_p]
             if L.origami_abi_version() != ABI_VERSION:
                 raise RuntimeError("liborigami_layout.so ABI version mismatch; rebuild it")
             _lib = L

@@ -1672,11 +1672,21 @@ int fill_plane_table(int64_t* table, const int64_t* offsets, const int64_t* spec
 // C ABI
 // ===========================================================================
 
+// A prepared fused restore (origami_restore_plan_create): everything but the
+// stream and cache pointers, shared read-only by every launch.
+struct origami_restore_plan {
+  std::shared_ptr<const Plan> plan;  // keeps a reordered plan's device table alive
+  RowsParams p;                      // stream and rows set per launch
+  int64_t stream_bytes = 0;          // chunk_offsets[num_chunks]
+  int64_t tokens = 0;
+  int device = 0;
+};
+
 extern "C" {
 
 const char* origami_last_error(void) { return g_last_error.c_str(); }
 
-int origami_abi_version(void) { return 2; }
+int origami_abi_version(void) { return 3; }
 
 int64_t origami_set_rows_grid_limit(int64_t max_workgroups) {
   const int64_t previous = g_rows_grid_limit;
@@ -1849,6 +1859,63 @@ int origami_unpack_canonical_to_kv_cache(
   return launch_rows(false, p, 2, plan->info.bits, rows_mode(plan->info, p, tokens, false),
                      stream);
 }
+
+int origami_restore_plan_create(const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
+                                const int64_t* chunk_specs, int64_t num_chunks, int64_t tokens,
+                                int64_t cache_layout, int64_t num_blocks, int64_t block_size,
+                                int64_t num_heads, int64_t head_bytes, const int64_t* block_ids,
+                                int64_t block_count, origami_restore_plan_t* out) {
+  ORIGAMI_REQUIRE(out != nullptr, "plan output pointer is null");
+  *out = nullptr;
+  ORIGAMI_REQUIRE(chunk_offsets != nullptr || num_chunks == 0, "chunk_offsets is null");
+  const int64_t need = num_chunks > 0 ? chunk_offsets[num_chunks] : 0;
+  int64_t blk_stride = 0, half_stride = 0;
+  // a 16-byte aligned stand-in for the cache pointer: the launch checks the real one
+  alignas(16) static const uint8_t kAligned[16] = {};
+  int rc = check_fused_restore(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, need,
+                               tokens, kAligned, cache_layout, num_blocks, block_size, num_heads,
+                               head_bytes, block_count, &blk_stride, &half_stride);
+  if (rc) return rc;
+  std::shared_ptr<const Plan> plan;
+  rc = get_plan(chunk_offsets, bits_per_chunk, chunk_specs, num_chunks, 2 * tokens, num_heads,
+                head_bytes, true, &plan);
+  if (rc) return rc;
+  if (!plan->has_table || !plan->info.regular || plan->info.bits == 0)
+    return fail(ORIGAMI_ERR_UNSUPPORTED,
+                "fused restore needs chunks spanning all tokens with one bit width");
+  auto rp = std::make_unique<origami_restore_plan>();
+  rp->plan = plan;
+  rp->stream_bytes = need;
+  rp->tokens = tokens;
+  if (hipGetDevice(&rp->device) != hipSuccess) return fail(ORIGAMI_ERR_HIP, "hipGetDevice failed");
+  rp->p = fused_restore_params(nullptr, 0, tokens, nullptr, num_blocks, block_size, num_heads,
+                               head_bytes, block_ids, block_count, blk_stride, half_stride);
+  if (int rc2 = set_planes(rp->p, plan)) return rc2;
+  set_grid_dims(rp->p, num_heads, head_bytes, rp->p.row_tokens, 2);
+  *out = rp.release();
+  return ORIGAMI_OK;
+}
+
+int origami_restore_plan_launch(origami_restore_plan_t plan, const uint8_t* flat_chunks,
+                                int64_t flat_bytes, void* kv_cache, origami_stream_t stream) {
+  ORIGAMI_REQUIRE(plan != nullptr, "restore plan is null");
+  ORIGAMI_REQUIRE(flat_chunks != nullptr || plan->stream_bytes == 0, "flat_chunks is null");
+  ORIGAMI_REQUIRE(flat_bytes >= plan->stream_bytes,
+                  "Origami CUDA packed chunk offsets exceed flat_chunks length");
+  ORIGAMI_REQUIRE(kv_cache != nullptr && aligned16(kv_cache),
+                  "fused restore needs a 16-byte aligned kv_cache");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev != plan->device)
+    return fail(ORIGAMI_ERR_INVALID, "restore plan launched on another device than it was made on");
+  RowsParams p = plan->p;
+  set_stream(p, flat_chunks, flat_bytes);
+  p.rows = static_cast<uint8_t*>(kv_cache);
+  return launch_rows(false, p, 2, plan->plan->info.bits,
+                     rows_mode(plan->plan->info, p, plan->tokens, false),
+                     reinterpret_cast<hipStream_t>(stream));
+}
+
+void origami_restore_plan_destroy(origami_restore_plan_t plan) { delete plan; }
 
 int origami_unpack_canonical_to_kv_cache_noalloc(
     const uint8_t* flat_chunks, int64_t flat_bytes, const int64_t* chunk_offsets,

@@ -376,6 +376,60 @@ bool unpack_canonical_to_kv_cache_batch(std::vector<at::Tensor> flats,
       current_stream(kv_cache)));
 }
 
+// A prepared restore (origami_restore_plan_create) with the cache geometry it
+// was made for and its device block table, which it keeps alive.
+struct PreparedRestore {
+  origami_restore_plan_t plan = nullptr;
+  std::vector<int64_t> sizes;
+  at::ScalarType dtype;
+  at::Device device;
+  at::Tensor block_ids;
+  ~PreparedRestore() { origami_restore_plan_destroy(plan); }
+};
+
+// Returns a handle (an integer), or 0 when the chunk plan is not served by the
+// fused kernel.
+int64_t restore_plan_create(at::Tensor chunk_offsets, at::Tensor bits_per_chunk,
+                            at::Tensor chunk_specs, int64_t tokens, at::Tensor kv_cache,
+                            at::Tensor block_ids) {
+  require_device(kv_cache, "kv_cache");
+  require_block_ids(block_ids, kv_cache);
+  const CacheGeom g = layout_cache_geometry(kv_cache);
+  const at::Tensor offs = host_i64(chunk_offsets), bits = host_i64(bits_per_chunk);
+  const at::Tensor specs = host_i64(chunk_specs);
+  TORCH_CHECK(offs.numel() == bits.numel() + 1, "chunk_offsets length must be chunk count + 1");
+  const c10::OptionalDeviceGuard guard(kv_cache.device());
+  origami_restore_plan_t plan = nullptr;
+  if (!check_supported(origami_restore_plan_create(
+          i64p(offs), i64p(bits), i64p(specs), bits.numel(), tokens, g.layout, g.num_blocks,
+          g.block_size, g.heads, g.head_bytes, block_ids.data_ptr<int64_t>(), block_ids.numel(),
+          &plan)))
+    return 0;
+  auto* r = new PreparedRestore{plan, kv_cache.sizes().vec(), kv_cache.scalar_type(),
+                                kv_cache.device(), block_ids};
+  return reinterpret_cast<int64_t>(r);
+}
+
+// One layer: `flat` (this layer's stream) into `kv_cache` (a cache of the
+// geometry the plan was made for), on the current stream.
+void restore_plan_launch(int64_t handle, const at::Tensor& flat, const at::Tensor& kv_cache) {
+  TORCH_CHECK(handle != 0, "restore plan is closed");
+  const auto* r = reinterpret_cast<const PreparedRestore*>(handle);
+  TORCH_CHECK(kv_cache.device() == r->device && kv_cache.scalar_type() == r->dtype &&
+                  kv_cache.sizes().equals(r->sizes) && kv_cache.is_contiguous(),
+              "kv_cache geometry differs from the prepared restore");
+  TORCH_CHECK(flat.device() == r->device && flat.scalar_type() == at::kByte &&
+                  flat.is_contiguous(),
+              "flat_chunks must be a contiguous uint8 tensor on the cache's device");
+  const c10::OptionalDeviceGuard guard(r->device);
+  check(origami_restore_plan_launch(r->plan, flat.data_ptr<uint8_t>(), flat.numel(),
+                                    kv_cache.data_ptr(), current_stream(kv_cache)));
+}
+
+void restore_plan_destroy(int64_t handle) {
+  delete reinterpret_cast<PreparedRestore*>(handle);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -391,5 +445,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("unpack_canonical_to_kv_cache", &unpack_canonical_to_kv_cache);
   m.def("pack_canonical_from_kv_cache", &pack_canonical_from_kv_cache);
   m.def("unpack_canonical_to_kv_cache_batch", &unpack_canonical_to_kv_cache_batch);
+  m.def("restore_plan_create", &restore_plan_create);
+  m.def("restore_plan_launch", &restore_plan_launch);
+  m.def("restore_plan_destroy", &restore_plan_destroy);
   m.def("abi_version", &origami_abi_version);
 }

@@ -401,6 +401,54 @@ class KVRestoreBatch:
             unpack_to_kv_cache(flat, layout, T, kv_cache, ids)  # irregular plans
 
 
+class PreparedRestore:
+    """The fused restore of one request prepared once for all of its layers:
+    the chunk plan, tokens, cache geometry and block table are checked and
+    looked up at construction, and restore(flat, kv_cache) then launches with
+    only the layer's stream and destination cache (origami_restore_plan_*).
+    The reference restores each layer through the full extension call
+    (worker.py:1087-1248); results equal unpack_to_kv_cache's.  `supported` is
+    False when the chunk plan is not served by the fused kernel; restore() then
+    takes unpack_to_kv_cache's two-step path.  Every kv_cache passed to
+    restore() must have the shape, dtype and device of the one given here."""
+
+    def __init__(self, layout: CanonicalLayout, tokens: int, kv_cache: torch.Tensor,
+                 block_ids):
+        _require_cuda(kv_cache, "kv_cache")
+        if (layout.token_count != 2 * tokens or kv_cache.dim() != 5
+                or layout.num_heads != kv_cache.shape[3]
+                or layout.head_dim != kv_cache.shape[4] * kv_cache.element_size()):
+            raise RuntimeError("symbol layout does not match the kv_cache geometry")
+        self.layout, self.tokens = layout, int(tokens)
+        self.block_ids = block_ids_tensor(block_ids, kv_cache.device,
+                                          cache_geometry(kv_cache)[1])
+        self._ext = _ext.ext()
+        self._handle = int(self._ext.restore_plan_create(*layout.torch_meta, self.tokens,
+                                                         kv_cache, self.block_ids))
+        self.supported = self._handle != 0
+
+    def restore(self, flat: torch.Tensor, kv_cache: torch.Tensor) -> None:
+        """Restores one layer's stream `flat` into `kv_cache` on the current stream."""
+        if self._handle:
+            self._ext.restore_plan_launch(self._handle, flat, kv_cache)
+        elif self.supported:
+            raise RuntimeError("restore plan is closed")
+        else:
+            unpack_to_kv_cache(flat, self.layout, self.tokens, kv_cache, self.block_ids)
+
+    def close(self) -> None:
+        """Frees the plan (work already enqueued keeps nothing of it)."""
+        h, self._handle = self._handle, 0
+        if h:
+            self._ext.restore_plan_destroy(h)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown
+            pass
+
+
 def unpack_batch_to_kv_cache(requests: Sequence[tuple], kv_cache: torch.Tensor, *,
                              dedup_shared_blocks: bool = False) -> None:
     """One layer of several requests, (flat stream, kv_symbol_layout, tokens,

@@ -142,8 +142,35 @@ def test_extension_module_exports_reference_names():
                  "kivi_dequantize_to_kv_cache_cuda", "fused_prefix_attention_cuda",
                  "unpack_canonical_to_kv_cache", "pack_canonical_from_kv_cache",
                  "unpack_canonical_to_kv_cache_batch", "pack_canonical_storage_chunks",
-                 "kivi_dequantize_to_kv_cache"):
+                 "kivi_dequantize_to_kv_cache", "restore_plan_create", "restore_plan_launch",
+                 "restore_plan_destroy"):
         assert callable(getattr(m, name)), name
     assert m.abi_version() == _native.ABI_VERSION
     with pytest.raises(RuntimeError, match="outside the layout path"):
         m.fused_prefix_attention_cuda()
+
+
+def test_restore_plan_host_checks():
+    """origami_restore_plan_create validates the chunk metadata and the cache
+    geometry before it needs a GPU, with the messages of the fused restore;
+    origami_restore_plan_launch refuses a null plan."""
+    specs = _native.i64_array([[0, 1, 0, 16, 0, 64], [0, 1, 16, 32, 0, 64]])
+    bits = _native.i64_array([8, 8])
+    out = ctypes.c_void_p()
+
+    def create(offsets, block_size=16, num_blocks=4, block_count=2):
+        offs = _native.i64_array(offsets)
+        return _native.call("origami_restore_plan_create", offs.ctypes.data, bits.ctypes.data,
+                            specs.ctypes.data, 2, 32, _native.CACHE_KV_FIRST, num_blocks,
+                            block_size, 1, 32, None, block_count, ctypes.byref(out))
+
+    with pytest.raises(_native.OrigamiNativeError, match="byte size mismatch"):
+        create([0, 1024, 2047])
+    with pytest.raises(_native.OrigamiNativeError, match="tokens exceed destination block"):
+        create([0, 1024, 2048], block_count=1)
+    with pytest.raises(_native.OrigamiNativeError, match="block size must be positive"):
+        create([0, 1024, 2048], block_size=0)
+    assert out.value is None
+    with pytest.raises(_native.OrigamiNativeError, match="restore plan is null"):
+        _native.call("origami_restore_plan_launch", None, None, 0, None, None)
+    _native.lib().origami_restore_plan_destroy(None)  # a null plan is a no-op
