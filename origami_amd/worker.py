@@ -189,16 +189,15 @@ class OrigamiConnectorWorker:
                 metrics_path=self.metrics_path, request_id=restore.request_id,
                 system="origami")
             start_perf = time.perf_counter()
-            # layers are issued in model order (the kv_caches order)
-            for layer_name, fut in layer_futures.items():
-                if fut.done():
-                    continue
-                try:
-                    result = self._restore_layer(restore, payload, layer_name, start_perf)
-                except Exception as exc:  # noqa: BLE001 - delivered through the future
-                    fut.set_exception(exc)
-                else:
-                    fut.set_result(result)
+            # fused restores prepared once per (plan, cache geometry, block
+            # table) for all layers of the request
+            prepared: dict = {}
+            try:
+                self._restore_layers_in_order(restore, payload, layer_futures, start_perf,
+                                              prepared)
+            finally:
+                for prep in prepared.values():
+                    prep.close()
             return restore.request_id
         except Exception as exc:
             for fut in layer_futures.values():
@@ -206,9 +205,25 @@ class OrigamiConnectorWorker:
                     fut.set_exception(exc)
             raise
 
+    def _restore_layers_in_order(self, restore: OrigamiRestoreRequest, payload: OrigamiPayload,
+                                 layer_futures: dict[str, Future], start_perf: float,
+                                 prepared: dict) -> None:
+        """Issues the request's layers in model order (the kv_caches order);
+        each layer's outcome goes to its future."""
+        for layer_name, fut in layer_futures.items():
+            if fut.done():
+                continue
+            try:
+                result = self._restore_layer(restore, payload, layer_name, start_perf,
+                                             prepared)
+            except Exception as exc:  # noqa: BLE001 - delivered through the future
+                fut.set_exception(exc)
+            else:
+                fut.set_result(result)
+
     def _restore_layer(self, restore: OrigamiRestoreRequest, payload: OrigamiPayload,
-                       layer_name: str, start_perf: float | None = None
-                       ) -> _LayerLoadResult | None:
+                       layer_name: str, start_perf: float | None = None,
+                       prepared: dict | None = None) -> _LayerLoadResult | None:
         layer_payload = payload.layer_payloads.get(layer_name)
         if layer_payload is None or layer_name not in self.kv_caches:
             return None
@@ -235,7 +250,7 @@ class OrigamiConnectorWorker:
             result = None
             if fmt == "raw_byte_planes" and kv_cache.is_cuda:
                 result = self._restore_byte_planes(restore, layer_payload, layout, kv_cache,
-                                                   block_ids, bs, nb, meta)
+                                                   block_ids, bs, nb, meta, group, prepared)
             elif fmt == "raw_bytes" and kv_cache.is_cuda and self._raw_bytes_scatterable(
                     meta, kv_cache, layout):
                 result = self._restore_raw_bytes(restore, layer_payload, layout, kv_cache,
@@ -312,18 +327,27 @@ class OrigamiConnectorWorker:
         return 2 * nblk * bs * H * D * kv_cache.element_size()
 
     def _restore_byte_planes(self, restore, layer_payload, layout, kv_cache, block_ids, bs, nb,
-                             meta):
+                             meta, group: int = 0, prepared: dict | None = None):
         tokens = int(meta.get("token_count", layout.token_count // 2))
         if layout.token_count != 2 * tokens:
             raise RuntimeError("raw_byte_planes symbol token axis must be 2 * token_count")
         needed = -(-tokens // bs)
         if len(block_ids) < needed:
             raise RuntimeError("tokens exceed destination block capacity")
-        ids_dev = native_gpu.block_ids_tensor(block_ids[:needed], kv_cache.device, nb)
+        # one prepared restore (plan, checks, device block table) serves every
+        # layer of the request with the same chunk plan and cache geometry
+        key = (group, tokens, tuple(kv_cache.shape), kv_cache.dtype, kv_cache.device,
+               layout.shape, layout.layout, layout.specs.tobytes(), layout.bits.tobytes())
+        prep = prepared.get(key) if prepared is not None else None
+        if prep is None:
+            prep = native_gpu.PreparedRestore(layout, tokens, kv_cache, block_ids[:needed])
+            if prepared is not None:
+                prepared[key] = prep
+        ids_dev = prep.block_ids
         written = self._written_bytes(kv_cache, needed)
         return self._submit_layer(
             restore, layer_payload, layout, kv_cache, ids_dev,
-            lambda flat: native_gpu.unpack_to_kv_cache(flat, layout, tokens, kv_cache, ids_dev),
+            lambda flat: prep.restore(flat, kv_cache),
             "bitunpack_cuda",
             {"backend": "hip_fused_unpack_scatter", "symbols": int(layout.symbol_count),
              "output_bytes": written, "bytes": int(layout.stream_bytes) + written})
