@@ -1,9 +1,12 @@
 """Layer-wise restore pipeline: overlapped copy + fused restore gives the same
-cache bytes as the direct restore, from pinned streams and from staging fills."""
+cache bytes as the direct restore and as the oracle's unpack + scatter
+(bitpack_layout_cuda.cu:91-128, benchmark_utils.py:350-444), from pinned
+streams and from staging fills."""
 import numpy as np
 import pytest
 import torch
 
+from oracle import oracle
 from origami_amd.layout import kv_symbol_layout
 from origami_amd.lossless import native_gpu
 from origami_amd.lossless.chunking import plan_head_channel_chunks
@@ -30,14 +33,18 @@ def test_pipeline_matches_direct_restore(cuda_device, mode):
     lay = kv_symbol_layout(T, H, C, 8, _specs(2 * T, H, C, 1 << 16))
     streams = [torch.randint(0, 256, (lay.stream_bytes,), dtype=torch.uint8, generator=g)
                for _ in range(L)]
-    ids = [native_gpu.block_ids_tensor(torch.randperm(NB, generator=g)[:nblk], cuda_device)
-           for _ in range(L)]
-    expect, got = [], []
+    ids_host = [torch.randperm(NB, generator=g)[:nblk] for _ in range(L)]
+    ids = [native_gpu.block_ids_tensor(i, cuda_device) for i in ids_host]
+    expect, got, oracle_caches = [], [], []
     for layer in range(L):
         c = torch.zeros((2, NB, bs, H, C), dtype=torch.uint8, device=cuda_device)
         native_gpu.unpack_to_kv_cache(streams[layer].to(cuda_device), lay, T, c, ids[layer])
         expect.append(c)
         got.append(torch.zeros_like(c))
+        o = np.zeros((2, NB, bs, H, C), dtype=np.uint8)
+        oracle.restore_layer(streams[layer].numpy(), lay.offsets, 8, lay.specs, T, H, C,
+                             ids_host[layer].numpy(), o)
+        oracle_caches.append(o)
     pipe = LayerRestorePipeline(cuda_device, lay.stream_bytes, num_slots=3)
     events = []
     pinned = [s.pin_memory() for s in streams]
@@ -52,3 +59,4 @@ def test_pipeline_matches_direct_restore(cuda_device, mode):
     for layer in range(L):
         torch.cuda.current_stream(cuda_device).wait_event(events[layer])
         assert torch.equal(got[layer], expect[layer]), layer
+        assert np.array_equal(got[layer].cpu().numpy(), oracle_caches[layer]), layer
