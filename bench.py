@@ -366,16 +366,18 @@ def dequant_leg(src_cache, T, bs, dst_cache, dst_ids, gen, dev, steps, layers=4)
     return legs
 
 
-def host_cost_leg(dev, calls=400, tokens=4096):
+def host_cost_leg(dev, calls=200, reps=7, tokens=4096):
     """Host time per restore call: wall time of `calls` back-to-back calls
     of one 4096-token layer (8 KV heads, head_dim 128, bf16, bs 16, planner
     chunks of 1 MiB) from Python, through native_gpu.unpack_to_kv_cache (the
     full entry point: tensor checks, chunk metadata, plan lookup) and through
-    a PreparedRestore made once for the request.  The loop is timed on the host
-    from a synchronized start without waiting for the GPU; `gpu_us_per_call`
-    (events over the same calls) shows the GPU was not what limited it."""
+    a PreparedRestore made once for the request.  Each of `reps` loops is
+    timed on the host from a synchronized start without waiting for the GPU;
+    the median is reported (and the fastest loop); `gpu_us_per_call` (events
+    over the same calls) shows the GPU was not what limited it."""
     import time
 
+    import numpy as np
     import torch
 
     from origami_amd.lossless import native_gpu
@@ -394,23 +396,29 @@ def host_cost_leg(dev, calls=400, tokens=4096):
     cache = torch.zeros_like(src)
     prep = native_gpu.PreparedRestore(layout, tokens, cache, ids)
     cur = torch.cuda.current_stream(dev)
-    out = {"calls": calls, "sample": f"one {tokens}-token layer, 8 KV heads, head_dim 128, bf16"}
+    out = {"calls": calls, "reps": reps,
+           "sample": f"one {tokens}-token layer, 8 KV heads, head_dim 128, bf16"}
     for name, fn in (("unpack_to_kv_cache", lambda: native_gpu.unpack_to_kv_cache(
                           flat, layout, tokens, cache, ids)),
                      ("prepared_restore", lambda: prep.restore(flat, cache))):
         for _ in range(50):
             fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(cur)
-        t0 = time.perf_counter()
-        for _ in range(calls):
-            fn()
-        t1 = time.perf_counter()
-        e1.record(cur)
-        torch.cuda.synchronize()
-        out[f"{name}_host_us"] = round((t1 - t0) * 1e6 / calls, 2)
-        out[f"{name}_gpu_us_per_call"] = round(e0.elapsed_time(e1) * 1e3 / calls, 2)
+        host, gpu = [], []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(cur)
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                fn()
+            t1 = time.perf_counter()
+            e1.record(cur)
+            torch.cuda.synchronize()
+            host.append((t1 - t0) * 1e6 / calls)
+            gpu.append(e0.elapsed_time(e1) * 1e3 / calls)
+        out[f"{name}_host_us"] = round(float(np.median(host)), 2)
+        out[f"{name}_host_us_min"] = round(min(host), 2)
+        out[f"{name}_gpu_us_per_call"] = round(float(np.median(gpu)), 2)
     ok = bool(torch.equal(cache.view(torch.uint8), src.view(torch.uint8)))
     out["restore_ok"] = ok
     prep.close()

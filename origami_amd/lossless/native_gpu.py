@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import functools
 from functools import lru_cache
 from typing import Iterable, Sequence
 
@@ -426,19 +427,21 @@ class PreparedRestore:
         self._handle = int(self._ext.restore_plan_create(*layout.torch_meta, self.tokens,
                                                          kv_cache, self.block_ids))
         self.supported = self._handle != 0
+        if self.supported:
+            # restore(flat, kv_cache) is the extension call itself: no Python
+            # frame of its own between the caller and the launch
+            self.restore = functools.partial(self._ext.restore_plan_launch, self._handle)
 
     def restore(self, flat: torch.Tensor, kv_cache: torch.Tensor) -> None:
         """Restores one layer's stream `flat` into `kv_cache` on the current stream."""
-        if self._handle:
-            self._ext.restore_plan_launch(self._handle, flat, kv_cache)
-        elif self.supported:
+        if self.supported:
             raise RuntimeError("restore plan is closed")
-        else:
-            unpack_to_kv_cache(flat, self.layout, self.tokens, kv_cache, self.block_ids)
+        unpack_to_kv_cache(flat, self.layout, self.tokens, kv_cache, self.block_ids)
 
     def close(self) -> None:
         """Frees the plan (work already enqueued keeps nothing of it)."""
         h, self._handle = self._handle, 0
+        self.__dict__.pop("restore", None)  # restore() now raises
         if h:
             self._ext.restore_plan_destroy(h)
 
