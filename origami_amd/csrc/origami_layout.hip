@@ -31,6 +31,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <unordered_map>
 #include <vector>
 
@@ -967,6 +968,132 @@ __global__ __launch_bounds__(kRowsThreads) void rows_unpack_batch_kernel(RowsBat
   }
 }
 
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>{});
+  }
+}
+
+// The lane one below in its DPP row (row_shr:1); lane 0 of a row reads 0.
+__device__ __forceinline__ uint32_t dpp_prev_lane(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x111, 0xf, 0xf, true));
+}
+
+// Bytes [sh, sh + 16) of the 32-byte little-endian value lo (bytes 0-15),
+// hi (bytes 16-31), for a per-lane 0 <= sh < 16.  The words are separate
+// scalars passed through an empty asm: selects between elements of an array
+// are turned into a run-time indexed read of it, which lives in scratch.
+__device__ __forceinline__ void funnel16(const uint32_t (&lo)[4], const uint32_t (&hi)[4],
+                                         int sh, uint32_t (&out)[4]) {
+  uint32_t w0 = lo[0], w1 = lo[1], w2 = lo[2], w3 = lo[3];
+  uint32_t w4 = hi[0], w5 = hi[1], w6 = hi[2], w7 = hi[3];
+  asm("" : "+v"(w0), "+v"(w1), "+v"(w2), "+v"(w3), "+v"(w4), "+v"(w5), "+v"(w6), "+v"(w7));
+  // a_j = w[8 * (sh >> 3) / 4 + j]: shift by 8 bytes when sh & 8
+  const bool q2 = (sh & 8) != 0, q1 = (sh & 4) != 0;
+  const uint32_t a0 = q2 ? w2 : w0, a1 = q2 ? w3 : w1, a2 = q2 ? w4 : w2;
+  const uint32_t a3 = q2 ? w5 : w3, a4 = q2 ? w6 : w4, a5 = q2 ? w7 : w5;
+  // u_j = a[j + (sh >> 2 & 1)]: shift by 4 more bytes when sh & 4
+  const uint32_t u0 = q1 ? a1 : a0, u1 = q1 ? a2 : a1, u2 = q1 ? a3 : a2;
+  const uint32_t u3 = q1 ? a4 : a3, u4 = q1 ? a5 : a4;
+  const uint32_t r = static_cast<uint32_t>(sh & 3);
+  out[0] = __builtin_amdgcn_alignbyte(u1, u0, r);
+  out[1] = __builtin_amdgcn_alignbyte(u2, u1, r);
+  out[2] = __builtin_amdgcn_alignbyte(u3, u2, r);
+  out[3] = __builtin_amdgcn_alignbyte(u4, u3, r);
+}
+
+// The dword of c holding byte j (0 <= j < 16), by selects on scalars (an
+// indexed read of c would put it in scratch memory).
+__device__ __forceinline__ uint32_t chunk_word(uint32_t c0, uint32_t c1, uint32_t c2,
+                                               uint32_t c3, int j) {
+  const uint32_t lo = (j & 4) ? c1 : c0, hi = (j & 4) ? c3 : c2;
+  return (j & 8) ? hi : lo;
+}
+
+// Writes bytes [lo, hi) of the 16-byte aligned chunk at dst (0 <= lo <= hi
+// <= 16; byte j of the chunk is byte j & 3 of c[j >> 2]): one 16-byte store for
+// a whole chunk, else at most a byte, a short, the whole dwords, a short and a
+// byte.
+__device__ __forceinline__ void store_chunk_bytes(uint8_t* dst, const uint32_t (&c)[4], int lo,
+                                                  int hi) {
+  if (lo == 0 && hi == 16) {
+    *reinterpret_cast<u32x4*>(dst) = u32x4{c[0], c[1], c[2], c[3]};
+    return;
+  }
+  uint32_t c0 = c[0], c1 = c[1], c2 = c[2], c3 = c[3];
+  asm("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3));
+  int a = lo;
+  if (a < hi && (a & 1)) {
+    dst[a] = static_cast<uint8_t>(chunk_word(c0, c1, c2, c3, a) >> (8 * (a & 3)));
+    ++a;
+  }
+  if (a + 2 <= hi && (a & 2)) {
+    *reinterpret_cast<uint16_t*>(dst + a) =
+        static_cast<uint16_t>(chunk_word(c0, c1, c2, c3, a) >> 16);
+    a += 2;
+  }
+  const uint32_t cw[4] = {c0, c1, c2, c3};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (4 * i >= a && 4 * i + 4 <= hi) *reinterpret_cast<uint32_t*>(dst + 4 * i) = cw[i];
+  int t = hi & ~3;
+  if (t < a) t = a;
+  if (t + 2 <= hi) {  // t is even here
+    *reinterpret_cast<uint16_t*>(dst + t) =
+        static_cast<uint16_t>(chunk_word(c0, c1, c2, c3, t) >> (8 * (t & 2)));
+    t += 2;
+  }
+  if (t < hi) dst[t] = static_cast<uint8_t>(chunk_word(c0, c1, c2, c3, t) >> (8 * (t & 3)));
+}
+
+// 8-bit pack at byte addresses (kRowsBytes): the 8 lanes of a group (lane & 7
+// = s) hold consecutive 16-token runs of each plane, lane s at a0 + 16 s.
+// Instead of each lane writing its run as head bytes, dwords and tail bytes,
+// lane s writes the 16-byte aligned chunk of the stream that begins in its
+// run: the last m bytes of lane s - 1's run (a DPP row shift) and the first
+// 16 - m of its own, m = a0 mod 16.  Lane 0 writes only the bytes of that chunk
+// from a0 on, the group's last lane also the bytes past its chunk;
+// neighbouring groups and halves write disjoint bytes of the chunks they
+// share.  Lanes past the half's last token have returned; they are never the
+// source of a shift (the active lanes of a group are s = 0 .. n - 1).
+__device__ __forceinline__ void store_runs8_realigned(const RowsParams& p, const TileCoord& tc,
+                                                      const int64_t* desc,
+                                                      const uint32_t (&v)[16][4]) {
+  const int s = static_cast<int>(threadIdx.x & 7);
+  const int64_t t0g = tc.t0 - 16 * s;  // the group's first token
+  const int L = static_cast<int>(p.T - t0g < 128 ? p.T - t0g : 128);  // group bytes per plane
+  const int last = (L + 15) / 16 - 1;  // the group's last active lane
+  const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
+  const uint32_t zero[4] = {0u, 0u, 0u, 0u};
+  // planes k = 0..15 written out at compile time (a loop over them was too
+  // large for the unroller, and a partly unrolled one indexed v at run time)
+  static_for<16>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const int64_t d = desc[tc.slot * 16 + k];
+    if (d < 0) return;  // uniform over the group
+    uint8_t* const at = p.stream + ((d + p.bit_bias + sym0 * 8) >> 3);
+    const int m = static_cast<int>(reinterpret_cast<uintptr_t>(at) & 15);  // uniform over the group
+    uint32_t prev[4], c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) prev[i] = dpp_prev_lane(v[k][i]);
+    funnel16(prev, v[k], (16 - m) & 15, c);
+    if (m == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[i] = v[k][i];
+    }
+    const int end = L - 16 * s + m;  // the group's end, relative to this lane's chunk
+    store_chunk_bytes(at - m, c, s == 0 ? m : 0, end < 16 ? end : 16);
+    if (s == last && end > 16) {  // m > 0 here
+      funnel16(v[k], zero, 16 - m, c);
+      store_chunk_bytes(at - m + 16, c, 0, end - 16);
+    }
+  });
+}
+
 template <int BITS, int MODE>
 __device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
                                           const int64_t* desc) {
@@ -997,6 +1124,10 @@ __device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
   uint32_t v[16][4];
   transpose16(r, v);
 
+  if constexpr (BITS == 8 && MODE == kRowsBytes) {
+    store_runs8_realigned(p, tc, desc, v);
+    return;
+  }
   constexpr int NU = (16 * BITS + 31) / 32;
   const int nbytes = (nv * BITS) >> 3;
   const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
