@@ -440,6 +440,9 @@ enum RowsMode : int {
   // (non-temporal loads here ran a 32784-token layer in 71.7 us, cached
   // ones in 64.1 us; on 128-byte lines non-temporal is faster: 53.8 vs 56.3).
   kRowsAligned16Cached = 5,
+  // pack, b = 8, runs not all on 128-byte lines: through LDS, each stream
+  // line written whole by one wave (rows_pack_staged8_kernel)
+  kRowsStaged8 = 6,
 };
 
 struct RowsParams {
@@ -977,35 +980,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// The lane one below in its DPP row (row_shr:1); lane 0 of a row reads 0.
-__device__ __forceinline__ uint32_t dpp_prev_lane(uint32_t x) {
-  return static_cast<uint32_t>(
-      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x111, 0xf, 0xf, true));
-}
-
-// Bytes [sh, sh + 16) of the 32-byte little-endian value lo (bytes 0-15),
-// hi (bytes 16-31), for a per-lane 0 <= sh < 16.  The words are separate
-// scalars passed through an empty asm: selects between elements of an array
-// are turned into a run-time indexed read of it, which lives in scratch.
-__device__ __forceinline__ void funnel16(const uint32_t (&lo)[4], const uint32_t (&hi)[4],
-                                         int sh, uint32_t (&out)[4]) {
-  uint32_t w0 = lo[0], w1 = lo[1], w2 = lo[2], w3 = lo[3];
-  uint32_t w4 = hi[0], w5 = hi[1], w6 = hi[2], w7 = hi[3];
-  asm("" : "+v"(w0), "+v"(w1), "+v"(w2), "+v"(w3), "+v"(w4), "+v"(w5), "+v"(w6), "+v"(w7));
-  // a_j = w[8 * (sh >> 3) / 4 + j]: shift by 8 bytes when sh & 8
-  const bool q2 = (sh & 8) != 0, q1 = (sh & 4) != 0;
-  const uint32_t a0 = q2 ? w2 : w0, a1 = q2 ? w3 : w1, a2 = q2 ? w4 : w2;
-  const uint32_t a3 = q2 ? w5 : w3, a4 = q2 ? w6 : w4, a5 = q2 ? w7 : w5;
-  // u_j = a[j + (sh >> 2 & 1)]: shift by 4 more bytes when sh & 4
-  const uint32_t u0 = q1 ? a1 : a0, u1 = q1 ? a2 : a1, u2 = q1 ? a3 : a2;
-  const uint32_t u3 = q1 ? a4 : a3, u4 = q1 ? a5 : a4;
-  const uint32_t r = static_cast<uint32_t>(sh & 3);
-  out[0] = __builtin_amdgcn_alignbyte(u1, u0, r);
-  out[1] = __builtin_amdgcn_alignbyte(u2, u1, r);
-  out[2] = __builtin_amdgcn_alignbyte(u3, u2, r);
-  out[3] = __builtin_amdgcn_alignbyte(u4, u3, r);
-}
-
 // The dword of c holding byte j (0 <= j < 16), by selects on scalars (an
 // indexed read of c would put it in scratch memory).
 __device__ __forceinline__ uint32_t chunk_word(uint32_t c0, uint32_t c1, uint32_t c2,
@@ -1014,20 +988,14 @@ __device__ __forceinline__ uint32_t chunk_word(uint32_t c0, uint32_t c1, uint32_
   return (j & 8) ? hi : lo;
 }
 
-// Writes bytes [lo, hi) of the 16-byte aligned chunk at dst (0 <= lo <= hi
-// <= 16; byte j of the chunk is byte j & 3 of c[j >> 2]): one 16-byte store for
-// a whole chunk, else at most a byte, a short, the whole dwords, a short and a
-// byte.
-__device__ __forceinline__ void store_chunk_bytes(uint8_t* dst, const uint32_t (&c)[4], int lo,
-                                                  int hi) {
-  if (lo == 0 && hi == 16) {
-    *reinterpret_cast<u32x4*>(dst) = u32x4{c[0], c[1], c[2], c[3]};
-    return;
-  }
-  uint32_t c0 = c[0], c1 = c[1], c2 = c[2], c3 = c[3];
+// Writes bytes [lo, hi) of the 16-byte aligned chunk at dst (0 <= lo < hi
+// <= 16, not the whole chunk; byte j of the chunk is byte j & 3 of c[j >> 2]):
+// at most a byte, a short, the whole dwords, a short and a byte.
+__device__ __forceinline__ void store_chunk_part(uint8_t* dst, uint32_t c0, uint32_t c1,
+                                                 uint32_t c2, uint32_t c3, int lo, int hi) {
   asm("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3));
   int a = lo;
-  if (a < hi && (a & 1)) {
+  if (a & 1) {
     dst[a] = static_cast<uint8_t>(chunk_word(c0, c1, c2, c3, a) >> (8 * (a & 3)));
     ++a;
   }
@@ -1050,58 +1018,10 @@ __device__ __forceinline__ void store_chunk_bytes(uint8_t* dst, const uint32_t (
   if (t < hi) dst[t] = static_cast<uint8_t>(chunk_word(c0, c1, c2, c3, t) >> (8 * (t & 3)));
 }
 
-// 8-bit pack at byte addresses (kRowsBytes): the 8 lanes of a group (lane & 7
-// = s) hold consecutive 16-token runs of each plane, lane s at a0 + 16 s.
-// Instead of each lane writing its run as head bytes, dwords and tail bytes,
-// lane s writes the 16-byte aligned chunk of the stream that begins in its
-// run: the last m bytes of lane s - 1's run (a DPP row shift) and the first
-// 16 - m of its own, m = a0 mod 16.  Lane 0 writes only the bytes of that chunk
-// from a0 on, the group's last lane also the bytes past its chunk;
-// neighbouring groups and halves write disjoint bytes of the chunks they
-// share.  Lanes past the half's last token have returned; they are never the
-// source of a shift (the active lanes of a group are s = 0 .. n - 1).
-__device__ __forceinline__ void store_runs8_realigned(const RowsParams& p, const TileCoord& tc,
-                                                      const int64_t* desc,
-                                                      const uint32_t (&v)[16][4]) {
-  const int s = static_cast<int>(threadIdx.x & 7);
-  const int64_t t0g = tc.t0 - 16 * s;  // the group's first token
-  const int L = static_cast<int>(p.T - t0g < 128 ? p.T - t0g : 128);  // group bytes per plane
-  const int last = (L + 15) / 16 - 1;  // the group's last active lane
-  const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
-  const uint32_t zero[4] = {0u, 0u, 0u, 0u};
-  // planes k = 0..15 written out at compile time (a loop over them was too
-  // large for the unroller, and a partly unrolled one indexed v at run time)
-  static_for<16>([&](auto kc) {
-    constexpr int k = decltype(kc)::value;
-    const int64_t d = desc[tc.slot * 16 + k];
-    if (d < 0) return;  // uniform over the group
-    uint8_t* const at = p.stream + ((d + p.bit_bias + sym0 * 8) >> 3);
-    const int m = static_cast<int>(reinterpret_cast<uintptr_t>(at) & 15);  // uniform over the group
-    uint32_t prev[4], c[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) prev[i] = dpp_prev_lane(v[k][i]);
-    funnel16(prev, v[k], (16 - m) & 15, c);
-    if (m == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) c[i] = v[k][i];
-    }
-    const int end = L - 16 * s + m;  // the group's end, relative to this lane's chunk
-    store_chunk_bytes(at - m, c, s == 0 ? m : 0, end < 16 ? end : 16);
-    if (s == last && end > 16) {  // m > 0 here
-      funnel16(v[k], zero, 16 - m, c);
-      store_chunk_bytes(at - m + 16, c, 0, end - 16);
-    }
-  });
-}
-
-template <int BITS, int MODE>
-__device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
-                                          const int64_t* desc) {
-  const TileCoord tc = tile_coord(p, ti);
-  if (tc.q >= p.nq || tc.t0 >= p.T) return;
-  const int nv = static_cast<int>(p.T - tc.t0 < 16 ? p.T - tc.t0 : 16);
-
-  uint32_t r[16][4];
+// Gathers a lane's 16 rows x 16 bytes (tokens t0 .. t0 + nv - 1 of its
+// 16-byte channel column) through the block table; missing rows read as 0.
+__device__ __forceinline__ void load_tile_rows(const RowsParams& p, const TileCoord& tc, int nv,
+                                               uint32_t (&r)[16][4]) {
   RowCursor rc;
   cursor_init(p, tc.t0, rc);
   const uint8_t* col = p.rows + static_cast<int64_t>(tc.h) * p.head_pitch + tc.q * 16;
@@ -1121,13 +1041,113 @@ __device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
       }
     }
   }
+}
+
+// 8-bit pack at byte addresses (kRowsBytes, b = 8), staged through LDS.
+// In a tile, the runs of one plane for one 16-channel slot are one stretch of
+// the stream: its region, bytes [R0, R0 + n) for the tile's n tokens.  Lanes
+// put their 16-token runs into LDS at their offset in the region; after a
+// barrier, wave wsi writes the region's 128-byte stream line wsi (and one
+// wave the line after the last), whole except where the region starts or
+// ends inside it.  Each line is then written by one wave.  Writing each run
+// in place instead leaves most lines written in two parts by two waves, which
+// measured 88.0 us per 32753-token layer against 59.7 us with the same work
+// on whole lines.  Planes go through LDS kStagePlanes at a time, in two
+// buffers, so one barrier per round separates writers and readers.
+constexpr int kStagePlanes = 4;
+constexpr int kStageFront = 16, kStageBack = 32;  // pad bytes around a region
+// A round: kStagePlanes x (wq * 8 slots) regions of ws * 128 + pad bytes, for
+// a workgroup of `waves` waves.
+constexpr int stage_round_bytes(int waves) {
+  return kStagePlanes * (waves * 1024 + kRowsWq * kLaneGroups * (kStageFront + kStageBack));
+}
+static_assert(2 * stage_round_bytes(kRowsMaxWaves) + kRowsWq * kWavePlanes * 8 <= 160 * 1024,
+              "LDS of the staged pack");
+
+// Writes this lane's 16-byte chunk of region line j: stream bytes
+// [line0 + 128 j + 16 s, + 16), region bytes [o, o + 16), o = 128 j + 16 s - M
+// (M = R0 mod 128); only the bytes inside the region [0, n).  Reads at most
+// 16 bytes before and 20 after the region's bytes in LDS (its pads).
+__device__ __forceinline__ void store_region_chunk(uint8_t* line0, const uint8_t* reg, int M,
+                                                   int n, int j, int s) {
+  const int o = 128 * j + 16 * s - M;
+  const int lo = o < 0 ? -o : 0, hi = n - o < 16 ? n - o : 16;
+  if (lo >= hi) return;
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(reg + (o & ~3));
+  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
+  const uint32_t sh = static_cast<uint32_t>(o & 3);
+  const uint32_t c0 = __builtin_amdgcn_alignbyte(w1, w0, sh);
+  const uint32_t c1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
+  const uint32_t c2 = __builtin_amdgcn_alignbyte(w3, w2, sh);
+  const uint32_t c3 = __builtin_amdgcn_alignbyte(w4, w3, sh);
+  uint8_t* const dst = line0 + 128 * j + 16 * s;
+  if (lo == 0 && hi == 16)
+    *reinterpret_cast<u32x4*>(dst) = u32x4{c0, c1, c2, c3};
+  else
+    store_chunk_part(dst, c0, c1, c2, c3, lo, hi);
+}
+
+// Every wave of the workgroup runs this for every tile (no early exit: the
+// rounds hold barriers); lanes outside the tile's channels or tokens only
+// take part in the barriers.
+template <int WAVES>
+__device__ __forceinline__ void pack_tile_staged8(const RowsParams& p, TileIndex ti,
+                                                  const int64_t* desc, uint8_t* stage) {
+  const TileCoord tc = tile_coord(p, ti);
+  const int s = static_cast<int>(threadIdx.x & 7);
+  const int wsi = static_cast<int>(threadIdx.x >> 6) / p.wq;
+  const int64_t T0 = tc.t0 - (static_cast<int64_t>(wsi) * kLaneSegs + s) * kSegTokens;
+  const bool slot_ok = tc.q < p.nq;
+  const bool run_ok = slot_ok && tc.t0 < p.T;
+  const int nv = run_ok ? static_cast<int>(p.T - tc.t0 < 16 ? p.T - tc.t0 : 16) : 0;
+
+  uint32_t r[16][4];
+  load_tile_rows(p, tc, nv, r);
   uint32_t v[16][4];
   transpose16(r, v);
 
-  if constexpr (BITS == 8 && MODE == kRowsBytes) {
-    store_runs8_realigned(p, tc, desc, v);
-    return;
-  }
+  const int n = static_cast<int>(p.T - T0 < p.ws * 128 ? p.T - T0 : p.ws * 128);
+  const int RS = p.ws * 128 + kStageFront + kStageBack;
+  const int slots = p.wq * kLaneGroups;
+  const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + T0;
+  const int run_off = kStageFront + (wsi * kLaneSegs + s) * kSegTokens;
+  static_for<16 / kStagePlanes>([&](auto rc) {
+    constexpr int round = decltype(rc)::value;
+    uint8_t* const buf = stage + (round & 1) * stage_round_bytes(WAVES);
+    static_for<kStagePlanes>([&](auto kc) {
+      constexpr int kk = decltype(kc)::value, k = round * kStagePlanes + kk;
+      if (run_ok && desc[tc.slot * 16 + k] >= 0)
+        *reinterpret_cast<u32x4*>(buf + (kk * slots + tc.slot) * RS + run_off) =
+            u32x4{v[k][0], v[k][1], v[k][2], v[k][3]};
+    });
+    __syncthreads();
+    static_for<kStagePlanes>([&](auto kc) {
+      constexpr int kk = decltype(kc)::value, k = round * kStagePlanes + kk;
+      const int64_t d = desc[tc.slot * 16 + k];
+      if (!slot_ok || d < 0) return;
+      uint8_t* const r0 = p.stream + ((d + p.bit_bias + sym0 * 8) >> 3);
+      const int M = static_cast<int>(reinterpret_cast<uintptr_t>(r0) & 127);
+      const uint8_t* const reg = buf + (kk * slots + tc.slot) * RS + kStageFront;
+      store_region_chunk(r0 - M, reg, M, n, wsi, s);
+      // the line past the waves' own (when the region is off a line): one
+      // wave per plane, a different one for each plane
+      if (wsi == (k & (p.ws - 1))) store_region_chunk(r0 - M, reg, M, n, p.ws, s);
+    });
+  });
+}
+
+template <int BITS, int MODE>
+__device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
+                                          const int64_t* desc) {
+  const TileCoord tc = tile_coord(p, ti);
+  if (tc.q >= p.nq || tc.t0 >= p.T) return;
+  const int nv = static_cast<int>(p.T - tc.t0 < 16 ? p.T - tc.t0 : 16);
+
+  uint32_t r[16][4];
+  load_tile_rows(p, tc, nv, r);
+  uint32_t v[16][4];
+  transpose16(r, v);
+
   constexpr int NU = (16 * BITS + 31) / 32;
   const int nbytes = (nv * BITS) >> 3;
   const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
@@ -1149,6 +1169,20 @@ __global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
     const TileIndex ti = split_tile(p, tile);
     load_descriptors(p, ti, desc);
     pack_tile<BITS, MODE>(p, ti, desc);
+  }
+}
+
+// The 8-bit pack off 128-byte lines (kRowsStaged8), for workgroups of WAVES
+// waves (p.waves == WAVES): LDS in proportion, so that the smaller workgroups
+// of short launches still share a CU.
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void rows_pack_staged8_kernel(RowsParams p) {
+  __shared__ int64_t desc[kRowsWq * kWavePlanes];
+  __shared__ __align__(16) uint8_t stage[2 * stage_round_bytes(WAVES)];
+  for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
+    const TileIndex ti = split_tile(p, tile);
+    load_descriptors(p, ti, desc);
+    pack_tile_staged8<WAVES>(p, ti, desc, stage);
   }
 }
 
@@ -1358,7 +1392,7 @@ int device_cu_count() {
 // workgroup is the largest of 16, 8 or 4 waves that still gives at least two
 // workgroups per CU over `nhalf` halves of `tile_tokens_total` tokens.
 void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_total,
-                   int64_t nhalf) {
+                   int64_t nhalf, int wq_max = kRowsWq) {
   if (H > 1 && p.head_pitch == C) {
     C *= H;
     H = 1;
@@ -1370,7 +1404,7 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
   const int64_t segs = (tile_tokens_total + kSegTokens - 1) / kSegTokens;
   const int64_t want = 2 * static_cast<int64_t>(device_cu_count());
   for (int waves = kRowsMaxWaves;; waves /= 2) {
-    const int wq_cap = waves == kRowsMaxWaves ? kRowsWq : 2;
+    const int wq_cap = std::min(waves == kRowsMaxWaves ? kRowsWq : 2, wq_max);
     int wq = 1;
     while (wq < wq_cap && wq * 2 <= nqg) wq *= 2;
     p.waves = waves;
@@ -1496,6 +1530,23 @@ int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack,
   return pack ? kRowsBytes : kRowsShift;
 }
 
+// Mode of the rows pack: 8-bit planes off 128-byte lines go through LDS so
+// that every stream line is written whole (32753 tokens: 3062 -> 3766 GB/s;
+// 32784, planes 32 bytes off: 3163 -> 3399).  Planes on lines keep in-place
+// non-temporal stores even when the V half is not: 3874 against 3608 staged
+// at 32832 tokens.
+int pack_mode(const PlanInfo& info, const RowsParams& p, int64_t T) {
+  const int mode = rows_mode(info, p, T, true);
+  if (info.bits == 8 && mode != kRowsAligned16) return kRowsStaged8;
+  return mode;
+}
+
+// Channel columns per workgroup tile of the staged pack: 1, 128 channels x
+// 2048 tokens, so a plane's region in a tile spans 17 lines, 2 of them shared
+// with the neighbouring tiles (3766 GB/s at 32753 tokens, against 3436 for
+// 256 x 1024 tiles).
+constexpr int kStagedWq = 1;
+
 // Restore launch in kRowsSplitWaves-wave workgroups, 2^sh per tile.
 int launch_rows_split(const RowsParams& p, int bits, int mode, hipStream_t stream) {
   int sh = 0;
@@ -1568,6 +1619,18 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
     else
       hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsAligned16Cached>), grid, block, 0, stream, p);
     return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
+  }
+  if (mode == kRowsStaged8) {
+    if (!pack || bits != 8) return fail(ORIGAMI_ERR_INVALID, "staged rows mode is the 8-bit pack");
+    if (p.waves == 16)
+      hipLaunchKernelGGL(rows_pack_staged8_kernel<16>, grid, block, 0, stream, p);
+    else if (p.waves == 8)
+      hipLaunchKernelGGL(rows_pack_staged8_kernel<8>, grid, block, 0, stream, p);
+    else if (p.waves == 4)
+      hipLaunchKernelGGL(rows_pack_staged8_kernel<4>, grid, block, 0, stream, p);
+    else
+      return fail(ORIGAMI_ERR_INVALID, "staged pack workgroups have 4, 8 or 16 waves");
+    return check_launch("rows_pack_staged8_kernel");
   }
   const bool window = mode == kRowsWindow;
 #define ORIGAMI_ROWS_CASE(B)                                                                  \
@@ -1947,8 +2010,9 @@ int origami_pack_canonical_storage_chunks(
     p.row_pitch = st.token;
     p.head_pitch = st.head;
     p.bs = T;
-    set_grid_dims(p, H, C, T, 1);
-    return launch_rows(true, p, 1, plan->info.bits, rows_mode(plan->info, p, T, true), stream);
+    const int mode = pack_mode(plan->info, p, T);
+    set_grid_dims(p, H, C, T, 1, mode == kRowsStaged8 ? kStagedWq : kRowsWq);
+    return launch_rows(true, p, 1, plan->info.bits, mode, stream);
   }
 
   rc = plan_device(plan);
@@ -2208,9 +2272,9 @@ int origami_pack_canonical_from_kv_cache(
   p.bs = block_size;
   p.blk_stride = blk_stride;
   p.half_stride = half_stride;
-  set_grid_dims(p, num_heads, head_bytes, tokens, 2);
-  return launch_rows(true, p, 2, plan->info.bits, rows_mode(plan->info, p, tokens, true),
-                     stream);
+  const int mode = pack_mode(plan->info, p, tokens);
+  set_grid_dims(p, num_heads, head_bytes, tokens, 2, mode == kRowsStaged8 ? kStagedWq : kRowsWq);
+  return launch_rows(true, p, 2, plan->info.bits, mode, stream);
 }
 
 static int block_copy(bool scatter, const uint8_t* src, uint8_t* dst, int64_t tokens,

@@ -5,7 +5,9 @@ boundaries.  Whether every run also starts on a 128-byte line (planes of
 2T bytes with 2T % 128 == 0, the V half at byte T with T % 128 == 0) picks
 non-temporal or cached accesses, and a token count that is not a multiple of
 the workgroup tile's 1024 tokens leaves a partial last token tile, which the
-restore orders after the full ones.  Each case packs one Llama-3-8B-geometry
+restore orders after the full ones.  The pack of planes off the lines goes
+through LDS (whole stream lines per wave) in 16-, 8- or 4-wave workgroups by
+launch size; odd token counts put runs at any byte.  Each case packs one Llama-3-8B-geometry
 layer (8 KV heads, head_dim 128, bf16, block size 16, permuted tables, 1 MiB
 planner chunks) from the paged cache and restores it into another cache; both
 must equal the oracle (chunking.py:22-123 for the plan,
@@ -40,6 +42,9 @@ def _oracle_threads():
     40000,   # planes 64 bytes off, partial last tile
     49216,   # planes on lines, V half off, partial last tile
     3088,    # small: 4-wave tiles, partial last tile
+    32753,   # odd: runs at any byte; staged pack in 16-wave tiles
+    16383,   # odd: staged pack in 8-wave tiles
+    4100,    # staged pack in 4-wave tiles, 4-token last tile
 ])
 @pytest.mark.parametrize("blocks_first", [False, True])
 def test_byte_planes_off_lines(cuda_device, T, blocks_first):
