@@ -54,6 +54,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=10)
     ap.add_argument("--no-pipeline", action="store_true")
+    ap.add_argument("--no-pack-ragged", action="store_true",
+                    help="skip the fused save at a ragged length (32753 tokens)")
     ap.add_argument("--no-dequant", action="store_true",
                     help="skip the CacheGen / KIVI fused dequantize legs")
     ap.add_argument("--no-configs", action="store_true",
@@ -271,6 +273,9 @@ def main() -> int:
         del host
         result["pipeline_llama3_70b_128k"] = pipeline_70b_leg(dev)
 
+    if not args.no_pack_ragged:
+        result["pack_ragged"] = pack_ragged_leg(dev, max(3, args.steps // 2), H=H, D=D, bs=bs)
+
     if not args.no_dequant:
         result["dequant"] = dequant_leg(src_cache, T, bs, torch.zeros_like(dst_caches[0]),
                                         dst_ids[0], gen, dev, args.steps)
@@ -288,6 +293,65 @@ def main() -> int:
                                               args.cpu_reps, dev)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def pack_ragged_leg(dev, steps, T=32753, layers=4, H=8, D=128, bs=16):
+    """Fused save (block gather + pack) at a ragged length: `layers` layers of
+    T tokens (odd, so runs start at any byte and the planes sit off 128-byte
+    lines; the 8-bit pack then stages through LDS), bf16, permuted source
+    tables, 1 MiB planner chunks, bits 8.  Bytes per layer: the stream, the
+    gathered blocks and the table.  Layer 0 is checked in closed form: its
+    stream is the plane-major transpose of its source tokens."""
+    import torch
+
+    from origami_amd.layout import kv_symbol_layout
+    from origami_amd.lossless import native_gpu
+    from origami_amd.lossless.chunking import plan_head_channel_chunks
+    from origami_amd.synthetic import fill_layer
+
+    C = 2 * D
+    nblk = -(-T // bs)
+    NB = nblk + nblk // 4
+    plan = plan_head_channel_chunks(layer_index=0, num_heads=H, head_dim=C, token_count=2 * T,
+                                    bytes_per_symbol=1, min_bytes=1 << 20,
+                                    target_bytes=1 << 20, max_bytes=1 << 20)
+    specs = [[c.layout.head_start, c.layout.head_end, c.layout.channel_start,
+              c.layout.channel_end, c.layout.token_start, c.layout.token_end] for c in plan]
+    layout = kv_symbol_layout(T, H, C, 8, specs)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    caches, ids, outs = [], [], []
+    for _ in range(layers):
+        c = torch.empty((2, NB, bs, H, D), dtype=torch.bfloat16, device=dev)
+        i = torch.randperm(NB, generator=gen, device=dev)[:nblk].contiguous()
+        fill_layer(c, i, gen)
+        caches.append(c)
+        ids.append(native_gpu.block_ids_tensor(i, dev, NB))
+        outs.append(torch.empty(layout.stream_bytes, dtype=torch.uint8, device=dev))
+
+    def one_pass():
+        for c, i, o in zip(caches, ids, outs):
+            native_gpu.pack_from_kv_cache(c, i, T, layout, o)
+
+    for _ in range(2):
+        one_pass()
+    cur = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(cur)
+    for _ in range(steps):
+        one_pass()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    layer_bytes = layout.stream_bytes + 2 * nblk * bs * H * C + 8 * nblk
+    src_tokens = caches[0].view(torch.uint8)[:, ids[0]].reshape(2, -1, H * C)[:, :T]
+    ok = bool(torch.equal(outs[0].view(H * C, 2 * T), src_tokens.reshape(2 * T, H * C).t()))
+    gbps = layers * layer_bytes / (ms * 1e-3) / 1e9
+    return {"tokens": T, "layers": layers, "us_per_layer": round(1e3 * ms / layers, 2),
+            "algorithmic_bytes_per_layer": layer_bytes, "gbps": round(gbps, 2),
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "pack_ok": ok,
+            "kernel": "rows_pack_staged8_kernel<16> (8-bit runs off 128-byte lines)"}
 
 
 def dequant_leg(src_cache, T, bs, dst_cache, dst_ids, gen, dev, steps, layers=4):
