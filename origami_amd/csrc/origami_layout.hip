@@ -85,6 +85,10 @@ namespace {
 // can be spread thinner over the GPU with it.
 thread_local int64_t g_rows_grid_limit = 0;
 
+// Batched restores of at least kRowsSplitTiles tiles per CU dispatch each
+// tile as 4-wave workgroups.
+constexpr bool kBatchSplit = true;
+
 // ---------------------------------------------------------------------------
 // Host-side layout helpers
 // ---------------------------------------------------------------------------
@@ -930,45 +934,62 @@ __global__ __launch_bounds__(kRowsSplitWaves * 64) void rows_unpack_split_kernel
 // the workgroup's tile picks its request with a uniform scan of at most
 // kBatchRequests tile offsets (a request with no tiles in a range has the next
 // request's offset, so the scan passes it).
+// Restores tile `tile` of a batched launch (slice `slice` of it with SPLIT).
+template <int BITS, int MODE, bool SPLIT>
+__device__ __forceinline__ void batch_tile(const RowsBatch& b, int64_t tile, int64_t* desc,
+                                           int slice) {
+  int r = 0;
+  TileIndex ti;
+  if (tile < b.nfull) {
+    while (r + 1 < b.nreq && tile >= b.req[r + 1].tile0) ++r;
+    const int full = b.req[r].nst - b.req[r].partial;
+    const int64_t local = tile - b.req[r].tile0;
+    ti = {static_cast<int>(local % full), local / full};
+  } else {
+    while (r + 1 < b.nreq && tile >= b.req[r + 1].ptile0) ++r;
+    ti = {b.req[r].nst - 1, tile - b.req[r].ptile0};
+  }
+  const RowsRequest& q = b.req[r];
+  RowsParams p = b.common;
+  p.stream = q.stream;
+  p.stream_bytes = q.stream_bytes;
+  p.bit_bias = q.bit_bias;
+  p.planes = q.planes;
+  p.plane_base = q.plane_base;
+  p.plane_bits = q.plane_bits;
+  p.block_ids = q.block_ids;
+  p.T = q.T;
+  p.row_tokens = q.row_tokens;
+  p.nst = q.nst;
+  p.token0 = q.token0;
+  load_descriptors(p, ti, desc);
+  if constexpr (MODE == kRowsAligned16) {
+    // one launch for the batch, the load policy per request
+    if (q.nt)
+      unpack_tile<BITS, kRowsAligned16, SPLIT>(p, ti, desc, slice);
+    else
+      unpack_tile<BITS, kRowsAligned16Cached, SPLIT>(p, ti, desc, slice);
+  } else {
+    unpack_tile<BITS, MODE, SPLIT>(p, ti, desc, slice);
+  }
+}
+
 template <int BITS, int MODE>
 __global__ __launch_bounds__(kRowsThreads) void rows_unpack_batch_kernel(RowsBatch b) {
   __shared__ int64_t desc[kTilePlanes];
-  for (int64_t tile = blockIdx.x; tile < b.common.ntiles; tile += gridDim.x) {
-    int r = 0;
-    TileIndex ti;
-    if (tile < b.nfull) {
-      while (r + 1 < b.nreq && tile >= b.req[r + 1].tile0) ++r;
-      const int full = b.req[r].nst - b.req[r].partial;
-      const int64_t local = tile - b.req[r].tile0;
-      ti = {static_cast<int>(local % full), local / full};
-    } else {
-      while (r + 1 < b.nreq && tile >= b.req[r + 1].ptile0) ++r;
-      ti = {b.req[r].nst - 1, tile - b.req[r].ptile0};
-    }
-    const RowsRequest& q = b.req[r];
-    RowsParams p = b.common;
-    p.stream = q.stream;
-    p.stream_bytes = q.stream_bytes;
-    p.bit_bias = q.bit_bias;
-    p.planes = q.planes;
-    p.plane_base = q.plane_base;
-    p.plane_bits = q.plane_bits;
-    p.block_ids = q.block_ids;
-    p.T = q.T;
-    p.row_tokens = q.row_tokens;
-    p.nst = q.nst;
-    p.token0 = q.token0;
-    load_descriptors(p, ti, desc);
-    if constexpr (MODE == kRowsAligned16) {
-      // one launch for the batch, the load policy per request
-      if (q.nt)
-        unpack_tile<BITS, kRowsAligned16>(p, ti, desc);
-      else
-        unpack_tile<BITS, kRowsAligned16Cached>(p, ti, desc);
-    } else {
-      unpack_tile<BITS, MODE>(p, ti, desc);
-    }
-  }
+  for (int64_t tile = blockIdx.x; tile < b.common.ntiles; tile += gridDim.x)
+    batch_tile<BITS, MODE, false>(b, tile, desc, 0);
+}
+
+// The batched restore with each tile dispatched as 2^sh workgroups of
+// kRowsSplitWaves waves, as rows_unpack_split_kernel does for one request.
+template <int BITS, int MODE>
+__global__ __launch_bounds__(kRowsSplitWaves * 64) void rows_unpack_batch_split_kernel(
+    RowsBatch b, int sh) {
+  __shared__ int64_t desc[kTilePlanes];
+  const int64_t slots = b.common.ntiles << sh;
+  for (int64_t s = blockIdx.x; s < slots; s += gridDim.x)
+    batch_tile<BITS, MODE, true>(b, s >> sh, desc, static_cast<int>(s & ((1 << sh) - 1)));
 }
 
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order.
@@ -1474,21 +1495,36 @@ void set_batch_grid(RowsBatch& b, int64_t H, int64_t C) {
 
 int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream) {
   if (b.common.ntiles <= 0) return ORIGAMI_OK;
-  int64_t blocks = b.common.ntiles;
+  // At least kRowsSplitTiles tiles per CU: each tile as 4-wave workgroups,
+  // as launch_rows does for one request.
+  int sh = 0;
+  if (kBatchSplit && b.common.waves > kRowsSplitWaves &&
+      b.common.ntiles >= kRowsSplitTiles * static_cast<int64_t>(device_cu_count()))
+    while ((kRowsSplitWaves << sh) < b.common.waves) ++sh;
+  const bool split = sh > 0;
+  int64_t blocks = b.common.ntiles << sh;
   if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
   if (blocks > INT32_MAX) blocks = INT32_MAX;
-  const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(64 * b.common.waves));
+  const dim3 grid(static_cast<unsigned>(blocks)),
+      block(static_cast<unsigned>(64 * (split ? kRowsSplitWaves : b.common.waves)));
+#define ORIGAMI_BATCH_LAUNCH(B, M)                                                              \
+  do {                                                                                          \
+    if (split)                                                                                  \
+      hipLaunchKernelGGL((rows_unpack_batch_split_kernel<B, M>), grid, block, 0, stream, b, sh); \
+    else                                                                                        \
+      hipLaunchKernelGGL((rows_unpack_batch_kernel<B, M>), grid, block, 0, stream, b);          \
+  } while (0)
   if (bits == 8 && mode == kRowsAligned16) {
-    hipLaunchKernelGGL((rows_unpack_batch_kernel<8, kRowsAligned16>), grid, block, 0, stream, b);
+    ORIGAMI_BATCH_LAUNCH(8, kRowsAligned16);
     return check_launch("rows_unpack_batch_kernel");
   }
   const bool window = mode == kRowsWindow;
-#define ORIGAMI_BATCH_CASE(B)                                                                    \
-  case B:                                                                                        \
-    if (window)                                                                                  \
-      hipLaunchKernelGGL((rows_unpack_batch_kernel<B, kRowsWindow>), grid, block, 0, stream, b); \
-    else                                                                                         \
-      hipLaunchKernelGGL((rows_unpack_batch_kernel<B, kRowsShift>), grid, block, 0, stream, b);  \
+#define ORIGAMI_BATCH_CASE(B)                  \
+  case B:                                      \
+    if (window)                                \
+      ORIGAMI_BATCH_LAUNCH(B, kRowsWindow);    \
+    else                                       \
+      ORIGAMI_BATCH_LAUNCH(B, kRowsShift);     \
     break;
   switch (bits) {
     ORIGAMI_BATCH_CASE(1)
@@ -1503,6 +1539,7 @@ int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream
       return fail(ORIGAMI_ERR_INVALID, "Origami CUDA bitpack supports only 1..8 bit symbols");
   }
 #undef ORIGAMI_BATCH_CASE
+#undef ORIGAMI_BATCH_LAUNCH
   return check_launch("rows_unpack_batch_kernel");
 }
 
