@@ -665,8 +665,6 @@ __device__ __forceinline__ void store_stream(uint8_t* dst, const uint32_t* u, in
   if constexpr (MODE == kRowsAligned16) {
     const u32x4 x = {u[0], u[1], u[2], u[3]};
     __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dst));
-  } else if constexpr (MODE == kRowsAligned16Cached) {
-    *reinterpret_cast<u32x4*>(dst) = u32x4{u[0], u[1], u[2], u[3]};
   } else if constexpr (MODE == kRowsWindow && BITS % 2 == 0) {
     if constexpr (NU == 1) {
       ORIGAMI_RUN_STORE(uint32_t, u[0], dst);
@@ -1064,7 +1062,7 @@ __device__ __forceinline__ void load_tile_rows(const RowsParams& p, const TileCo
   }
 }
 
-// 8-bit pack at byte addresses (kRowsBytes, b = 8), staged through LDS.
+// 8-bit pack of planes off 128-byte lines (kRowsStaged8), staged through LDS.
 // In a tile, the runs of one plane for one 16-channel slot are one stretch of
 // the stream: its region, bytes [R0, R0 + n) for the tile's n tokens.  Lanes
 // put their 16-token runs into LDS at their offset in the region; after a
@@ -1554,7 +1552,8 @@ int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack,
       // Non-temporal when every plane starts on a 128-byte line and, for the
       // restore, the V half too (T % 128 == 0).  The pack kept non-temporal
       // stores faster with only the V half off the line: 4136 against 3794
-      // GB/s at T = 32832; with planes off the line, 2359 against 3160 at 32784.
+      // GB/s at T = 32832.  (A pack of planes off the line is staged through
+      // LDS instead: pack_mode.)
       const bool lines = info.lines128 && (reinterpret_cast<uintptr_t>(p.stream) & 127) == 0;
       // Lane runs start at token0 + 16 k: a batched request restored past
       // its shared prefix needs token0 % 128 == 0 too.
@@ -1650,12 +1649,11 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
       hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsAligned16>), grid, block, 0, stream, p);
     return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
   }
+  if (pack && bits == 8 && mode != kRowsStaged8)  // pack_mode: aligned16 or staged
+    return fail(ORIGAMI_ERR_INVALID, "8-bit rows pack modes are aligned16 and staged");
   if (bits == 8 && mode == kRowsAligned16Cached) {
-    if (pack)
-      hipLaunchKernelGGL((rows_pack_kernel<8, kRowsAligned16Cached>), grid, block, 0, stream, p);
-    else
-      hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsAligned16Cached>), grid, block, 0, stream, p);
-    return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
+    hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsAligned16Cached>), grid, block, 0, stream, p);
+    return check_launch("rows_unpack_kernel");
   }
   if (mode == kRowsStaged8) {
     if (!pack || bits != 8) return fail(ORIGAMI_ERR_INVALID, "staged rows mode is the 8-bit pack");
@@ -1692,7 +1690,12 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
     ORIGAMI_ROWS_CASE(5)
     ORIGAMI_ROWS_CASE(6)
     ORIGAMI_ROWS_CASE(7)
-    ORIGAMI_ROWS_CASE(8)
+    case 8:  // restore only: the 8-bit pack is aligned16 or staged
+      if (window)
+        hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsWindow>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsShift>), grid, block, 0, stream, p);
+      break;
     default:
       return fail(ORIGAMI_ERR_INVALID, "Origami CUDA bitpack supports only 1..8 bit symbols");
   }
