@@ -52,7 +52,7 @@ from origami_amd.metadata import (
 )
 from origami_amd.quantization import QuantizerAdapter, create_quantizer_adapter
 from origami_amd.quantization.raw_tensor import RawBytePlanesAdapter
-from origami_amd.restore_pipeline import LayerRestorePipeline, LayerTiming, PipelineRegistry
+from origami_amd.restore_pipeline import LayerRestorePipeline, PipelineRegistry
 from origami_amd.store import OrigamiStore
 
 _NATIVE_LAYOUT_KEY = "origami_native_layout"

@@ -10,7 +10,6 @@ import pytest
 from oracle import oracle
 from origami_amd import _native
 from origami_amd.lossless.chunking import plan_head_channel_chunks
-from tests import bitref
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "origami_layout.h"
 

@@ -12,7 +12,6 @@ import torch
 
 from oracle import oracle
 from origami_amd.connector import KVConnectorRole, OrigamiConnector
-from origami_amd.lossless import native_gpu
 from origami_amd.metadata import (OrigamiConnectorMetadata, OrigamiRestoreRequest,
                                   OrigamiSaveRequest)
 

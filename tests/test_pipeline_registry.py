@@ -3,7 +3,6 @@ while leased or busy; event-timed metric rows are written once their events
 complete (worker.py:574-617)."""
 import json
 import threading
-import time
 
 import pytest
 
