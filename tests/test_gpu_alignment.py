@@ -85,3 +85,35 @@ def test_byte_planes_off_lines(cuda_device, T, blocks_first):
     oracle.restore_layer(flat, offs, 8, specs, T, H, C, dt, expect, blocks_first=blocks_first)
     assert np.array_equal(dst.view(torch.uint8).cpu().numpy(), expect), \
         "restore differs from the oracle"
+
+
+@pytest.mark.parametrize("shift", [5, 16, 77])
+def test_staged_pack_into_offset_stream(cuda_device, shift):
+    """The staged 8-bit pack of a full 32753-token layer (16-wave workgroups)
+    written `shift` bytes into a larger buffer: the stream equals the oracle's
+    and the bytes around it keep their guard value (the lines at the
+    stream's ends are partial)."""
+    dev, C, T = cuda_device, D * 2, 32753
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(shift)
+    nblk = -(-T // BS)
+    NB = nblk + 11
+    src = torch.zeros((2, NB, BS, H, D), dtype=torch.bfloat16, device=dev)
+    fill_layer(src, torch.arange(NB, device=dev), gen)
+    st = np.random.default_rng(shift).permutation(NB)[:nblk].astype(np.int64)
+    plan = plan_head_channel_chunks(layer_index=0, num_heads=H, head_dim=C, token_count=2 * T,
+                                    bytes_per_symbol=1, min_bytes=1 << 20,
+                                    target_bytes=1 << 20, max_bytes=1 << 20)
+    specs = [[c.layout.head_start, c.layout.head_end, c.layout.channel_start,
+              c.layout.channel_end, c.layout.token_start, c.layout.token_end] for c in plan]
+    lay = kv_symbol_layout(T, H, C, 8, specs)
+    buf = torch.full((lay.stream_bytes + shift + 131,), 0xA5, dtype=torch.uint8, device=dev)
+    native_gpu.pack_from_kv_cache(src, native_gpu.block_ids_tensor(st, dev, NB), T, lay,
+                                  buf[shift:shift + lay.stream_bytes])
+    host = buf.cpu().numpy()
+    sym = oracle.gather_kv_cache(src.view(torch.uint8).cpu().numpy(), st)
+    sym = sym.reshape(2, -1, H, C)[:, :T].reshape(-1)
+    flat, _ = oracle.pack_canonical(sym, 8, specs, [2 * T, H, C], [0, 1, 2, -1])
+    assert np.array_equal(host[shift:shift + lay.stream_bytes], flat), "pack differs from the oracle"
+    assert (host[:shift] == 0xA5).all() and (host[shift + lay.stream_bytes:] == 0xA5).all(), \
+        "bytes outside the stream were written"
