@@ -184,6 +184,8 @@ struct PlanInfo {
   bool planes_even = false;  // every plane starts on a 2-byte boundary
   bool planes_dword = false; // every plane starts on a 4-byte boundary
   bool lines128 = false;     // every plane starts on a 128-byte line (b = 8)
+  bool planes16 = false;     // every plane starts on a 16-byte boundary (any b)
+  bool planes_lines = false; // every plane starts on a 128-byte line (any b)
   // Every plane p = h * C + c is covered and starts at bit dense_base + p * T *
   // bits: the plane table is a closed form (what the chunk planner produces),
   // so the row kernels compute descriptors instead of reading a table.
@@ -207,6 +209,7 @@ PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
   info.planes_even = true;
   info.planes_dword = true;
   info.lines128 = true;
+  info.planes16 = info.planes_lines = true;
   for (int64_t k = 0; k < n; ++k) {
     const int64_t* s = specs + 6 * k;
     if (bits[k] != info.bits) info.bits = 0;
@@ -222,8 +225,8 @@ PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
         int64_t& slot = table[h * C + c];
         if (slot != -1) info.regular = false;
         slot = bit_off;
-        if (bit_off % 128 != 0) info.aligned16 = false;
-        if (bit_off % 1024 != 0) info.lines128 = false;
+        if (bit_off % 128 != 0) info.aligned16 = info.planes16 = false;
+        if (bit_off % 1024 != 0) info.lines128 = info.planes_lines = false;
         if (bit_off % 8 != 0) info.byte_aligned = false;
         if (bit_off % 16 != 0) info.planes_even = false;
         if (bit_off % 32 != 0) info.planes_dword = false;
@@ -232,9 +235,11 @@ PlanInfo build_plane_table(const int64_t* offsets, const int64_t* bits,
   }
   if (info.bits != 8) info.aligned16 = false;
   if (!info.aligned16) info.lines128 = false;
+  if (!info.planes16) info.planes_lines = false;
   if (!info.regular) {
     info.aligned16 = false;
     info.lines128 = false;
+    info.planes16 = info.planes_lines = false;
     info.byte_aligned = false;
     info.planes_even = false;
     info.planes_dword = false;
@@ -447,6 +452,11 @@ enum RowsMode : int {
   // pack, b = 8, runs not all on 128-byte lines: through LDS, each stream
   // line written whole by one wave (rows_pack_staged8_kernel)
   kRowsStaged8 = 6,
+  // restore, b = 1, 2 or 4, runs on 16-byte boundaries, T % (128 / b) == 0:
+  // 16-byte runs of 128 / b tokens per lane (rows_unpack_wide_kernel),
+  // non-temporal when every group's 8 runs are one 128-byte line
+  kRowsWide = 7,
+  kRowsWideCached = 8,
 };
 
 struct RowsParams {
@@ -770,7 +780,8 @@ __device__ __forceinline__ TileIndex split_tile(const RowsParams& p, int64_t til
 // fastest; with SPLIT, workgroup `slice` holds waves [4 slice, 4 slice + 4)
 // and wave tiles run along tokens fastest, so a workgroup is one channel
 // column of the tile.
-template <bool SPLIT = false>
+// SEG: tokens of a lane's run (16; 128 / b in the wide restore).
+template <bool SPLIT = false, int SEG = kSegTokens>
 __device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, TileIndex ti,
                                                 int slice = 0) {
   const int st = ti.st;
@@ -793,7 +804,7 @@ __device__ __forceinline__ TileCoord tile_coord(const RowsParams& p, TileIndex t
   }
   tc.slot = wqi * kLaneGroups + (lane >> 3);
   tc.q = qt * p.wq * kLaneGroups + tc.slot;
-  tc.t0 = p.token0 + (static_cast<int64_t>(st * p.ws + wsi) * kLaneSegs + (lane & 7)) * kSegTokens;
+  tc.t0 = p.token0 + (static_cast<int64_t>(st * p.ws + wsi) * kLaneSegs + (lane & 7)) * SEG;
   return tc;
 }
 
@@ -924,6 +935,90 @@ __global__ __launch_bounds__(kRowsSplitWaves * 64) void rows_unpack_split_kernel
     const TileIndex ti = split_tile(p, tile);
     load_descriptors(p, ti, desc);
     unpack_tile<BITS, MODE, true>(p, ti, desc, static_cast<int>(s & ((1 << sh) - 1)));
+  }
+}
+
+// Restore at b = 1, 2 or 4 with runs on 16-byte boundaries (kRowsWide): a
+// lane's run of a plane is one 16-byte load, 128 / b tokens, so the 8 lanes
+// of a group read a whole 128-byte line per plane (the window mode reads 2b
+// bytes per lane: at b = 4 two waves each read half of every line).  The lane
+// then restores its run as 16-token sub-tiles: expand, transpose, 16 row
+// stores each.  Needs T % (128 / b) == 0, so a run holds symbols either
+// throughout or not at all.
+template <int BITS, bool NT>
+__device__ __forceinline__ void unpack_tile_wide(const RowsParams& p, TileIndex ti,
+                                                 const int64_t* desc) {
+  static_assert(BITS == 1 || BITS == 2 || BITS == 4, "wide runs are 16 bytes of 1, 2 or 4-bit symbols");
+  constexpr int SEG = 128 / BITS, SUB = SEG / kSegTokens;
+  const TileCoord tc = tile_coord<false, SEG>(p, ti);
+  if (tc.q >= p.nq || tc.t0 >= p.row_tokens) return;
+  const bool has_symbols = tc.t0 < p.T;
+  const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
+
+  uint32_t w[16][4];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t d = desc[tc.slot * 16 + k];
+    w[k][0] = w[k][1] = w[k][2] = w[k][3] = 0;
+    if (d >= 0 && has_symbols) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(p.stream + ((d + p.bit_bias + sym0 * BITS) >> 3));
+      const u32x4 x = NT ? __builtin_nontemporal_load(src) : *src;
+      w[k][0] = x.x;
+      w[k][1] = x.y;
+      w[k][2] = x.z;
+      w[k][3] = x.w;
+    }
+  }
+  uint8_t* const col = p.rows + static_cast<int64_t>(tc.h) * p.head_pitch + tc.q * 16;
+#pragma unroll
+  for (int m = 0; m < SUB; ++m) {
+    const int64_t t0 = tc.t0 + m * kSegTokens;
+    if (t0 >= p.row_tokens) break;
+    // sub-tile m: bits [16 b m, 16 b (m + 1)) of each run
+    uint32_t v[16][4];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      uint32_t u[2];
+      if constexpr (BITS == 4) {
+        u[0] = w[k][2 * m];
+        u[1] = w[k][2 * m + 1];
+      } else if constexpr (BITS == 2) {
+        u[0] = w[k][m];
+      } else {
+        u[0] = w[k][m >> 1] >> (16 * (m & 1));
+      }
+      expand16<BITS>(u, v[k]);
+    }
+    uint32_t o[16][4];
+    transpose16(v, o);
+    RowCursor rc;
+    cursor_init(p, t0, rc);
+    const int64_t nrows = p.row_tokens - t0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (j < nrows) {
+        if (j > 0) cursor_next(p, rc);
+        const int64_t row = cursor_row(p, tc.half, rc);
+        if (row >= 0) {
+          const u32x4 x = {o[j][0], o[j][1], o[j][2], o[j][3]};
+          __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(col + row * p.row_pitch));
+        }
+      }
+    }
+  }
+}
+
+// Wide-run workgroups have at most kWideMaxWaves waves: the 16-byte runs of
+// 16 planes stay in registers while the sub-tiles are restored.
+constexpr int kWideMaxWaves = 8;
+
+template <int BITS, bool NT>
+__global__ __launch_bounds__(kWideMaxWaves * 64) void rows_unpack_wide_kernel(RowsParams p) {
+  __shared__ int64_t desc[kTilePlanes];
+  for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
+    const TileIndex ti = split_tile(p, tile);
+    load_descriptors(p, ti, desc);
+    unpack_tile_wide<BITS, NT>(p, ti, desc);
   }
 }
 
@@ -1411,7 +1506,8 @@ int device_cu_count() {
 // workgroup is the largest of 16, 8 or 4 waves that still gives at least two
 // workgroups per CU over `nhalf` halves of `tile_tokens_total` tokens.
 void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_total,
-                   int64_t nhalf, int wq_max = kRowsWq) {
+                   int64_t nhalf, int wq_max = kRowsWq, int seg_tokens = kSegTokens,
+                   int max_waves = kRowsMaxWaves) {
   if (H > 1 && p.head_pitch == C) {
     C *= H;
     H = 1;
@@ -1420,9 +1516,9 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
   p.C = C;
   p.nq = static_cast<int32_t>(C / 16);
   const int nqg = (p.nq + kLaneGroups - 1) / kLaneGroups;
-  const int64_t segs = (tile_tokens_total + kSegTokens - 1) / kSegTokens;
+  const int64_t segs = (tile_tokens_total + seg_tokens - 1) / seg_tokens;
   const int64_t want = 2 * static_cast<int64_t>(device_cu_count());
-  for (int waves = kRowsMaxWaves;; waves /= 2) {
+  for (int waves = max_waves;; waves /= 2) {
     const int wq_cap = std::min(waves == kRowsMaxWaves ? kRowsWq : 2, wq_max);
     int wq = 1;
     while (wq < wq_cap && wq * 2 <= nqg) wq *= 2;
@@ -1546,7 +1642,16 @@ int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream
 // plane).  The rows pack is only launched for byte-aligned planes with T * b
 // a multiple of 8, so its runs always start on bytes.
 int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack,
-              int64_t token0 = 0) {
+              int64_t token0 = 0, bool allow_wide = false) {
+  if (allow_wide && !pack && p.bit_bias == 0 && aligned16(p.stream) && info.planes16 &&
+      (info.bits == 1 || info.bits == 2 || info.bits == 4)) {
+    const int64_t seg = 128 / info.bits;
+    if (T % seg == 0 && token0 % seg == 0) {
+      const bool lines = info.planes_lines && (reinterpret_cast<uintptr_t>(p.stream) & 127) == 0 &&
+                         (T * info.bits) % 1024 == 0 && (token0 * info.bits) % 1024 == 0;
+      return lines ? kRowsWide : kRowsWideCached;
+    }
+  }
   if (p.bit_bias == 0 && T % 16 == 0) {
     if (info.aligned16 && aligned16(p.stream)) {
       // Non-temporal when every plane starts on a 128-byte line and, for the
@@ -1564,6 +1669,16 @@ int rows_mode(const PlanInfo& info, const RowsParams& p, int64_t T, bool pack,
     if (runs_ok) return kRowsWindow;
   }
   return pack ? kRowsBytes : kRowsShift;
+}
+
+// Workgroup grid of a single-request restore in `mode`: wide runs hold
+// 128 / b tokens and their workgroups at most kWideMaxWaves waves.
+void set_restore_grid(RowsParams& p, int mode, int bits, int64_t H, int64_t C,
+                      int64_t tile_tokens_total, int64_t nhalf) {
+  if (mode == kRowsWide || mode == kRowsWideCached)
+    set_grid_dims(p, H, C, tile_tokens_total, nhalf, kRowsWq, 128 / bits, kWideMaxWaves);
+  else
+    set_grid_dims(p, H, C, tile_tokens_total, nhalf);
 }
 
 // Mode of the rows pack: 8-bit planes off 128-byte lines go through LDS so
@@ -1635,6 +1750,31 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
   // partial token tiles last: restore 32784 tokens 64.0 -> 61.4 us, 49216
   // tokens 96.8 -> 94.8 us; the pack ran 2-5% slower that way
   if (pack) p.partial_last = 0;
+  if (mode == kRowsWide || mode == kRowsWideCached) {
+    if (pack || p.waves > kWideMaxWaves)
+      return fail(ORIGAMI_ERR_INVALID, "wide rows mode is a restore of at most 8-wave tiles");
+    int64_t blocks = p.ntiles;
+    if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
+    if (blocks > INT32_MAX) blocks = INT32_MAX;
+    const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(64 * p.waves));
+    const bool nt = mode == kRowsWide;
+#define ORIGAMI_WIDE_CASE(B)                                                                \
+  case B:                                                                                   \
+    if (nt)                                                                                 \
+      hipLaunchKernelGGL((rows_unpack_wide_kernel<B, true>), grid, block, 0, stream, p);    \
+    else                                                                                    \
+      hipLaunchKernelGGL((rows_unpack_wide_kernel<B, false>), grid, block, 0, stream, p);   \
+    break;
+    switch (bits) {
+      ORIGAMI_WIDE_CASE(1)
+      ORIGAMI_WIDE_CASE(2)
+      ORIGAMI_WIDE_CASE(4)
+      default:
+        return fail(ORIGAMI_ERR_INVALID, "wide rows mode takes 1, 2 or 4-bit symbols");
+    }
+#undef ORIGAMI_WIDE_CASE
+    return check_launch("rows_unpack_wide_kernel");
+  }
   if (!pack && p.waves > kRowsSplitWaves &&
       p.ntiles >= kRowsSplitTiles * static_cast<int64_t>(device_cu_count()))
     return launch_rows_split(p, bits, mode, stream);
@@ -1791,6 +1931,7 @@ PlanInfo analyze_plan(const int64_t* offsets, const int64_t* bits, const int64_t
   info.bits = n > 0 ? static_cast<int>(bits[0]) : 0;
   info.aligned16 = info.byte_aligned = info.planes_even = info.planes_dword = true;
   info.lines128 = true;
+  info.planes16 = info.planes_lines = true;
   bool in_order = true;  // chunk k holds planes [next, next + planes_k) in h * C + c order
   int64_t next = 0;
   for (int64_t k = 0; k < n; ++k) {
@@ -1803,8 +1944,8 @@ PlanInfo analyze_plan(const int64_t* offsets, const int64_t* bits, const int64_t
     const int64_t planes = (s[1] - s[0]) * (s[3] - s[2]);
     const int64_t first = offsets[k] * 8, step = T * bits[k];
     auto all_multiple = [&](int64_t m) { return first % m == 0 && (planes == 1 || step % m == 0); };
-    if (!all_multiple(128)) info.aligned16 = false;
-    if (!all_multiple(1024)) info.lines128 = false;
+    if (!all_multiple(128)) info.aligned16 = info.planes16 = false;
+    if (!all_multiple(1024)) info.lines128 = info.planes_lines = false;
     if (!all_multiple(8)) info.byte_aligned = false;
     if (!all_multiple(16)) info.planes_even = false;
     if (!all_multiple(32)) info.planes_dword = false;
@@ -1829,9 +1970,11 @@ PlanInfo analyze_plan(const int64_t* offsets, const int64_t* bits, const int64_t
   }
   if (info.bits != 8) info.aligned16 = false;
   if (!info.aligned16) info.lines128 = false;
+  if (!info.planes16) info.planes_lines = false;
   if (!info.regular) {
     info.aligned16 = info.byte_aligned = info.planes_even = info.planes_dword = false;
     info.lines128 = false;
+    info.planes16 = info.planes_lines = false;
   }
   if (info.regular && info.bits != 0 && in_order && next == H * C && H * C > 0) {
     info.dense = true;
@@ -1998,9 +2141,9 @@ int origami_unpack_canonical_storage_chunks(
     p.bs = T;
     p.blk_stride = 0;
     p.half_stride = 0;
-    set_grid_dims(p, H, C, T, 1);
-    return launch_rows(false, p, 1, plan->info.bits, rows_mode(plan->info, p, T, false),
-                       stream);
+    const int mode = rows_mode(plan->info, p, T, false, 0, true);
+    set_restore_grid(p, mode, plan->info.bits, H, C, T, 1);
+    return launch_rows(false, p, 1, plan->info.bits, mode, stream);
   }
 
   rc = launch_fill_zero(output, output_bytes, stream);
@@ -2090,9 +2233,9 @@ int origami_unpack_canonical_to_kv_cache(
                                       block_size, num_heads, head_bytes, block_ids, block_count,
                                       blk_stride, half_stride);
   if (int rc2 = set_planes(p, plan)) return rc2;
-  set_grid_dims(p, num_heads, head_bytes, p.row_tokens, 2);
-  return launch_rows(false, p, 2, plan->info.bits, rows_mode(plan->info, p, tokens, false),
-                     stream);
+  const int mode = rows_mode(plan->info, p, tokens, false, 0, true);
+  set_restore_grid(p, mode, plan->info.bits, num_heads, head_bytes, p.row_tokens, 2);
+  return launch_rows(false, p, 2, plan->info.bits, mode, stream);
 }
 
 int origami_restore_plan_create(const int64_t* chunk_offsets, const int64_t* bits_per_chunk,
