@@ -85,10 +85,6 @@ namespace {
 // can be spread thinner over the GPU with it.
 thread_local int64_t g_rows_grid_limit = 0;
 
-// Batched restores of at least kRowsSplitTiles tiles per CU dispatch each
-// tile as 4-wave workgroups.
-constexpr bool kBatchSplit = true;
-
 // ---------------------------------------------------------------------------
 // Host-side layout helpers
 // ---------------------------------------------------------------------------
@@ -1592,7 +1588,7 @@ int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream
   // At least kRowsSplitTiles tiles per CU: each tile as 4-wave workgroups,
   // as launch_rows does for one request.
   int sh = 0;
-  if (kBatchSplit && b.common.waves > kRowsSplitWaves &&
+  if (b.common.waves > kRowsSplitWaves &&
       b.common.ntiles >= kRowsSplitTiles * static_cast<int64_t>(device_cu_count()))
     while ((kRowsSplitWaves << sh) < b.common.waves) ++sh;
   const bool split = sh > 0;
