@@ -427,7 +427,56 @@ def dequant_leg(src_cache, T, bs, dst_cache, dst_ids, gen, dev, steps, layers=4)
         del payloads
     del kvs, dsts
     torch.cuda.empty_cache()
+    legs["cachegen_dense"] = _cachegen_dense_leg(T, H, D, dev, steps, layers)
     return legs
+
+
+def _cachegen_dense_leg(T, H, D, dev, steps, layers):
+    """CacheGen unpack + dequantize into the float16 [layers, 2, H, T, D]
+    tensor (cachegen_dense_kernel, one launch per K or V stream segment):
+    `layers` layers at 4-bit keys and values, 16 bins, float16 per-token
+    maxima.  The streams are zeros, so every value must come out as minus
+    its token's maximum (symbol 0 dequantizes to (0 - c) / c * max, c = 7),
+    which checks the output in closed form.  Algorithmic bytes: the streams,
+    the maxima and the float16 output."""
+    import torch
+
+    from origami_amd.lossless import native_gpu
+
+    seg = T * H * D * 4 // 8
+    offs = torch.arange(2 * layers + 1, dtype=torch.int64) * seg
+    stream = torch.zeros(2 * layers * seg, dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    mk = (torch.rand(layers * T, generator=g, device=dev) * 2 + 0.1).half()
+    mv = (torch.rand(layers * T, generator=g, device=dev) * 2 + 0.1).half()
+    bits = torch.full((2 * layers,), 4, dtype=torch.int64)
+    bins = torch.full((layers,), 16, dtype=torch.int64)
+
+    def run():
+        return native_gpu.cachegen_unpack_dequantize(stream, offs, bits, bins, bins, mk, mv,
+                                                     tokens=T, heads=H, head_dim=D)
+
+    out = run()
+    ok = bool(torch.equal(out[:, 0], (-mk).view(layers, 1, T, 1).expand(-1, H, -1, D))
+              and torch.equal(out[:, 1], (-mv).view(layers, 1, T, 1).expand(-1, H, -1, D)))
+    del out
+    run()
+    cur = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(cur)
+    for _ in range(steps):
+        run()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (steps * layers)
+    alg = 2 * seg + 2 * T * 2 + 2 * H * T * D * 2
+    gbps = alg / (ms * 1e-3) / 1e9
+    return {"kernel": "cachegen_dense_kernel<4> (float16 [L, 2, H, T, D] output)",
+            "bits": [4, 4], "layers": layers, "per_layer_us": round(ms * 1e3, 2),
+            "algorithmic_bytes_per_layer": int(alg), "gbps": round(gbps, 2),
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "output_ok": ok}
 
 
 def host_cost_leg(dev, calls=200, reps=7, tokens=4096):
