@@ -55,17 +55,17 @@ def _tables(perm, nblks, shared, pool):
     return out
 
 
-def _run(dev, H, D, dtype, lengths, seed, shared_pool, expect_chunks=None, batch=False):
+def _run(dev, H, D, dtype, lengths, seed, shared_pool, expect_chunks=None, batch=False, bs=BS):
     esize = torch.empty((), dtype=dtype).element_size()
     C = D * esize
     rng = np.random.default_rng(seed)
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    nblks = [-(-int(T) // BS) for T in lengths]
-    shared = [int(T) // 2 // BS if shared_pool else 0 for T in lengths]
+    nblks = [-(-int(T) // bs) for T in lengths]
+    shared = [int(T) // 2 // bs if shared_pool else 0 for T in lengths]
     pool = max(shared) if shared_pool else 0
     NB = pool + sum(n - k for n, k in zip(nblks, shared)) + 64
-    src = torch.zeros((2, NB, BS, H, D), dtype=dtype, device=dev)
+    src = torch.zeros((2, NB, bs, H, D), dtype=dtype, device=dev)
     fill_layer(src, torch.arange(NB, device=dev), gen)
     src_tables = _tables(rng.permutation(NB), nblks, shared, pool)
     dst_tables = _tables(rng.permutation(NB), nblks, shared, pool)
@@ -129,12 +129,22 @@ def test_llama3_70b_131072_full(cuda_device):
     _run(cuda_device, 8, 128, torch.bfloat16, [131072], 4, False, expect_chunks=512)
 
 
-@pytest.mark.parametrize("T,bits", [(131067, 8), (131072, 4), (131072, 3), (131061, 5)])
-def test_large_single_request_split_launch(cuda_device, T, bits):
+def test_batch_split_launch_block_size_24(cuda_device):
+    """The fp8 batch (16 x 16384 tokens, 4-wave workgroups per tile) with
+    24-token blocks and a shared prefix pool: a lane's 16 rows cross block
+    boundaries, so the restore follows the block table row by row."""
+    _run(cuda_device, 8, 128, torch.float8_e4m3fn, [16384] * 16, 5, True, batch=True, bs=24)
+
+
+@pytest.mark.parametrize("T,bits,bs", [(131067, 8, 16), (131072, 4, 16), (131072, 3, 16),
+                                       (131061, 5, 16), (131072, 8, 24), (131061, 4, 8)])
+def test_large_single_request_split_launch(cuda_device, T, bits, bs):
     """One ~131072-token layer (8 heads, 256-byte head rows, 2048 tiles: the
     restore launch that dispatches each tile as 4-wave workgroups) in the
     shift (ragged T) and window (sub-byte widths) addressing modes, against the
-    oracle's unpack + scatter of the oracle's pack."""
+    oracle's unpack + scatter of the oracle's pack.  With 16-token blocks a
+    lane's 16 rows lie in one block; 24- and 8-token blocks take the
+    row-by-row walk of the block table."""
     dev, H, C = cuda_device, 8, 256
     rng = np.random.default_rng(T + bits)
     plan = plan_head_channel_chunks(layer_index=0, num_heads=H, head_dim=C, token_count=2 * T,
@@ -146,12 +156,12 @@ def test_large_single_request_split_launch(cuda_device, T, bits):
     sym = rng.integers(0, 256, 2 * T * H * C, dtype=np.uint8)
     flat, offs = oracle.pack_canonical(sym, bits, specs, [2 * T, H, C], [0, 1, 2, -1])
     del sym
-    nblk = -(-T // BS)
+    nblk = -(-T // bs)
     NB = nblk + 64
     table = rng.permutation(NB)[:nblk].astype(np.int64)
-    dst = torch.zeros((2, NB, BS, H, C // 2), dtype=torch.bfloat16, device=dev)
+    dst = torch.zeros((2, NB, bs, H, C // 2), dtype=torch.bfloat16, device=dev)
     native_gpu.unpack_to_kv_cache(torch.from_numpy(flat).to(dev), lay, T, dst,
                                   native_gpu.block_ids_tensor(table, dev, NB))
-    expect = np.zeros((2, NB, BS, H, C), dtype=np.uint8)
+    expect = np.zeros((2, NB, bs, H, C), dtype=np.uint8)
     oracle.restore_layer(flat, offs, bits, specs, T, H, C, table, expect)
-    assert np.array_equal(dst.view(torch.uint8).cpu().numpy(), expect.reshape(2, NB, BS, H, C))
+    assert np.array_equal(dst.view(torch.uint8).cpu().numpy(), expect.reshape(2, NB, bs, H, C))
