@@ -255,7 +255,7 @@ def main() -> int:
             "traffic_source": ("profiles/rows_unpack_llama3_8b_32k.txt: EA read/write requests "
                                "by size from rocprofv3 --pmc runs of bench.py --profile-only "
                                "(not measured in this run)"),
-            "kernel": "rows_unpack_kernel<8, 2> (b = 8, 16-byte aligned runs)",
+            "kernel": "rows_unpack_kernel<8, 2, false, false> (b = 8, 16-byte aligned runs)",
             "avg_launch_us": round(avg_launch_ms * 1e3, 2),
         },
         "pack_gbps": round(pack_gbps, 2),
@@ -351,7 +351,7 @@ def pack_ragged_leg(dev, steps, T=32753, layers=4, H=8, D=128, bs=16):
     return {"tokens": T, "layers": layers, "us_per_layer": round(1e3 * ms / layers, 2),
             "algorithmic_bytes_per_layer": layer_bytes, "gbps": round(gbps, 2),
             "frac": round(gbps / HBM_PEAK_GBPS, 4), "pack_ok": ok,
-            "kernel": "rows_pack_staged8_kernel<16> (8-bit runs off 128-byte lines)"}
+            "kernel": "rows_pack_staged8_kernel<16, false> (8-bit runs off 128-byte lines)"}
 
 
 def dequant_leg(src_cache, T, bs, dst_cache, dst_ids, gen, dev, steps, layers=4):
@@ -958,7 +958,7 @@ def committed_traffic(args):
     if not default or not TRAFFIC_FILE.exists():
         return None
     for line in TRAFFIC_FILE.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch rows_unpack_kernel<8, 2>:"):
+        if line.startswith("traffic_bytes_per_launch rows_unpack_kernel<8, 2, false, false>:"):
             return int(line.split(":")[1].split()[0])
     return None
 

@@ -597,67 +597,140 @@ __device__ __forceinline__ void load_run_dwords(const uint8_t* src, uint32_t* w)
   }
 }
 
-// Loads the 16 symbols starting at stream bit P into 16 bytes.
-template <int BITS, int MODE>
-__device__ __forceinline__ void load_symbols16(const RowsParams& p, int64_t P,
-                                               uint32_t (&out)[4]) {
-  if constexpr (MODE == kRowsAligned16 || MODE == kRowsAligned16Cached) {
-    static_assert(BITS == 8, "aligned loads are for 8-bit symbols");
-    // the stream is read once: non-temporal when each 8-lane run is one line
-    const u32x4* src = reinterpret_cast<const u32x4*>(p.stream + (P >> 3));
-    const u32x4 x = MODE == kRowsAligned16 ? __builtin_nontemporal_load(src) : *src;
-    out[0] = x.x;
-    out[1] = x.y;
-    out[2] = x.z;
-    out[3] = x.w;
-  } else {
-    constexpr int NU = (16 * BITS + 31) / 32;  // = ceil(b / 2): dwords of a run
-    uint32_t u[NU > 4 ? NU : 4];
-    bool loaded = false;
-    if constexpr (MODE == kRowsWindow) {
-      // The run's 2b bytes start on an even byte (on a dword when b is even),
-      // so the NU dwords from the dword at or below it hold the whole run.
-      const int64_t byte0 = (P >> 3) & ~int64_t(3);
-      if (byte0 + 4 * NU <= p.stream_bytes) {
-        uint32_t w[NU + 1];
-        load_run_dwords<NU>(p.stream + byte0, w);
-        w[NU] = 0;
-        const uint32_t sh = (BITS % 2 == 1 && ((P >> 3) & 2)) ? 16u : 0u;
+// The window and shift modes of load_planes16 (below).
+template <int BITS, int MODE, bool SERIAL>
+__device__ __forceinline__ void load_runs16(const RowsParams& p, const int64_t* desc,
+                                            int64_t sym0, bool any, uint32_t (&v)[16][4]) {
+  static_assert(MODE == kRowsWindow || MODE == kRowsShift, "restore addressing mode");
+  constexpr int NU = (16 * BITS + 31) / 32;  // = ceil(b / 2): dwords of a run
+  // kRowsWindow: the run's 2b bytes start on an even byte (on a dword when b
+  // is even), so the NU dwords from the dword at or below it hold it.
+  // kRowsShift: the run starts at any bit, so the NU + 1 dwords from the one
+  // holding its first bit hold it.
+  constexpr int NW = MODE == kRowsShift ? NU + 1 : NU;
+  if constexpr (SERIAL) {
 #pragma unroll
-        for (int i = 0; i < NU; ++i) u[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sh);
-        loaded = true;
-      }
-    }
-    if constexpr (MODE == kRowsShift) {
-      // The run's 16b bits start at any bit: the NU + 1 dwords from the one
-      // holding its first bit hold it.
-      constexpr int NB = NU + 1;
-      const int64_t byte0 = (P >> 5) * 4;
-      if (byte0 + 4 * NB <= p.stream_bytes) {
-        uint32_t w[5];
-        if constexpr (NB == 5) {
+    for (int k = 0; k < 16; ++k) {
+      const int64_t d = desc[k];
+      v[k][0] = v[k][1] = v[k][2] = v[k][3] = 0;
+      if (d < 0 || !any) continue;
+      const int64_t P = d + p.bit_bias + sym0 * BITS;
+      const int64_t byte0 = MODE == kRowsShift ? (P >> 5) * 4 : (P >> 3) & ~int64_t(3);
+      uint32_t w[NU + 1], u[NU > 4 ? NU : 4];
+      uint32_t sh;
+      if (byte0 + 4 * NW <= p.stream_bytes) {
+        if constexpr (NW == 5) {
           load_run_dwords<4>(p.stream + byte0, w);
           load_run_dwords<1>(p.stream + byte0 + 16, w + 4);
         } else {
-          load_run_dwords<NB>(p.stream + byte0, w);
+          load_run_dwords<NW>(p.stream + byte0, w);
         }
-        const uint32_t sh = static_cast<uint32_t>(P & 31);
+        if constexpr (NW == NU) w[NU] = 0;
+        sh = MODE == kRowsShift ? static_cast<uint32_t>(P & 31)
+             : (BITS % 2 == 1 && ((P >> 3) & 2)) ? 16u
+                                                 : 0u;
+      } else {  // as below: the NU + 1 dwords from the one holding bit P
+        const int64_t d0 = P >> 5;
+        sh = static_cast<uint32_t>(P & 31);
 #pragma unroll
-        for (int i = 0; i < NU; ++i) u[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sh);
-        loaded = true;
+        for (int i = 0; i <= NU; ++i)
+          w[i] = load_dword_guarded(p.stream, (d0 + i) * 4, p.stream_bytes);
       }
-    }
-    if (!loaded) {  // the window would pass the end of the stream
-      constexpr int NW = NU + 1;
-      const int64_t d0 = P >> 5;
-      const uint32_t sh = static_cast<uint32_t>(P & 31);
-      uint32_t w[NW];
-#pragma unroll
-      for (int i = 0; i < NW; ++i) w[i] = load_dword_guarded(p.stream, (d0 + i) * 4, p.stream_bytes);
 #pragma unroll
       for (int i = 0; i < NU; ++i) u[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], sh);
+      expand16<BITS>(u, v[k]);
     }
-    expand16<BITS>(u, out);
+  } else {
+    uint32_t w[16][NW];
+    uint32_t tail = 0;    // bit k: plane k's dwords pass the end of the stream
+    uint32_t shp[4] = {};  // byte k & 3 of shp[k >> 2]: plane k's funnel shift
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int64_t d = desc[k];
+#pragma unroll
+      for (int i = 0; i < NW; ++i) w[k][i] = 0;
+      if (d >= 0 && any) {
+        const int64_t P = d + p.bit_bias + sym0 * BITS;
+        const int64_t byte0 = MODE == kRowsShift ? (P >> 5) * 4 : (P >> 3) & ~int64_t(3);
+        const uint32_t sh = MODE == kRowsShift ? static_cast<uint32_t>(P & 31)
+                            : (BITS % 2 == 1 && ((P >> 3) & 2)) ? 16u
+                                                                : 0u;
+        shp[k >> 2] |= sh << (8 * (k & 3));
+        if (byte0 + 4 * NW <= p.stream_bytes) {
+          if constexpr (NW == 5) {
+            load_run_dwords<4>(p.stream + byte0, w[k]);
+            load_run_dwords<1>(p.stream + byte0 + 16, w[k] + 4);
+          } else {
+            load_run_dwords<NW>(p.stream + byte0, w[k]);
+          }
+        } else {
+          tail |= 1u << k;
+        }
+      }
+    }
+    // keeps the descriptors from staying live in registers until the tail
+    // reloads below (they are read from LDS again there)
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      uint32_t u[NU > 4 ? NU : 4];
+      if (tail & (1u << k)) {
+        // the NU + 1 dwords from the one holding bit P, those past the end of
+        // the stream read as zeros
+        const int64_t P = desc[k] + p.bit_bias + sym0 * BITS;
+        const int64_t d0 = P >> 5;
+        const uint32_t sh = static_cast<uint32_t>(P & 31);
+        uint32_t t[NU + 1];
+#pragma unroll
+        for (int i = 0; i <= NU; ++i)
+          t[i] = load_dword_guarded(p.stream, (d0 + i) * 4, p.stream_bytes);
+#pragma unroll
+        for (int i = 0; i < NU; ++i) u[i] = __builtin_amdgcn_alignbit(t[i + 1], t[i], sh);
+      } else {
+        const uint32_t sh = (shp[k >> 2] >> (8 * (k & 3))) & 31u;
+#pragma unroll
+        for (int i = 0; i < NU; ++i)
+          u[i] = __builtin_amdgcn_alignbit(i + 1 < NW ? w[k][i + 1] : 0u, w[k][i], sh);
+      }
+      expand16<BITS>(u, v[k]);
+    }
+  }
+}
+
+// Loads a lane's 16 symbols of each of its 16 planes (plane k at stream bit
+// P_k = desc[k] + bit_bias + sym0 * b; a plane with desc[k] < 0, or every
+// plane when `any` is false, reads as zeros) into v[k], one byte per symbol.
+// Every plane's dwords are requested before any of them is used, so a lane
+// has all 16 loads in flight at once: with the funnel shift of each plane
+// next to its loads, the compiler waited for every plane's data before
+// requesting the next plane's (16 round trips per lane, 2053 tokens restored
+// in 15.9 us against 8.5 for 2048).  A run whose dwords would pass the end
+// of the stream is read again dword by dword afterwards.  SERIAL keeps the
+// funnel shift next to each plane's loads (window and shift modes): with two
+// loads per plane (b = 7, 8 in shift mode) and more than 12 waves per CU that
+// order restored faster (15000 tokens 28.2 us, against 30.5 with every load
+// in flight).
+template <int BITS, int MODE, bool SERIAL = false>
+__device__ __forceinline__ void load_planes16(const RowsParams& p, const int64_t* desc,
+                                              int64_t sym0, bool any, uint32_t (&v)[16][4]) {
+  if constexpr (MODE == kRowsAligned16 || MODE == kRowsAligned16Cached) {
+    static_assert(BITS == 8, "aligned loads are for 8-bit symbols");
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int64_t d = desc[k];
+      v[k][0] = v[k][1] = v[k][2] = v[k][3] = 0;
+      if (d >= 0 && any) {
+        // the stream is read once: non-temporal when each 8-lane run is one line
+        const u32x4* src = reinterpret_cast<const u32x4*>(p.stream + ((d + p.bit_bias + sym0 * 8) >> 3));
+        const u32x4 x = MODE == kRowsAligned16 ? __builtin_nontemporal_load(src) : *src;
+        v[k][0] = x.x;
+        v[k][1] = x.y;
+        v[k][2] = x.z;
+        v[k][3] = x.w;
+      }
+    }
+  } else {
+    load_runs16<BITS, MODE, SERIAL>(p, desc, sym0, any, v);
   }
 }
 
@@ -861,10 +934,12 @@ __device__ __forceinline__ int64_t cursor_row(const RowsParams& p, int half, con
 // consecutive rows of one block: one table load, then fixed strides.
 // Otherwise a cursor follows the table; its table load, taken only when the
 // rows cross into the next block, makes the compiler wait for every
-// outstanding memory access of the wave (stores included) before each row.
-// That wait costs the 4-wave restore workgroups 2-8% (131072 tokens of
-// Llama-3-70B geometry: 0.601 -> 0.649 of HBM peak), and the 16- and 8-wave
-// workgroups run 1-4% faster with it.
+// outstanding memory access of the wave (stores included) before each row,
+// so a lane's 16 row accesses go one at a time.  That costs the split
+// restores 2-8% (131072 tokens of Llama-3-70B geometry: 0.601 -> 0.649 of
+// HBM peak) and launches of few waves per CU up to half their time, while
+// whole-tile launches of 8 or more waves per CU run 1-4% faster with it: the
+// host picks by launch size (waves_per_cu).
 template <bool ONEBLK, class F>
 __device__ __forceinline__ void for_rows16(const RowsParams& p, int half, int64_t t0,
                                            int64_t nrows, F&& f) {
@@ -892,7 +967,7 @@ __device__ __forceinline__ void for_rows16(const RowsParams& p, int half, int64_
 // Rows kernels
 // ---------------------------------------------------------------------------
 
-template <int BITS, int MODE, bool SPLIT = false, bool ONEBLK = false>
+template <int BITS, int MODE, bool SPLIT = false, bool ONEBLK = false, bool SERIAL = false>
 __device__ __forceinline__ void unpack_tile(const RowsParams& p, TileIndex ti,
                                             const int64_t* desc, int slice = 0) {
   const TileCoord tc = tile_coord<SPLIT>(p, ti, slice);
@@ -901,15 +976,7 @@ __device__ __forceinline__ void unpack_tile(const RowsParams& p, TileIndex ti,
   const int64_t sym0 = static_cast<int64_t>(tc.half) * p.T + tc.t0;
 
   uint32_t v[16][4];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int64_t d = desc[tc.slot * 16 + k];
-    if (d < 0 || nv <= 0) {
-      v[k][0] = v[k][1] = v[k][2] = v[k][3] = 0;
-    } else {
-      load_symbols16<BITS, MODE>(p, d + p.bit_bias + sym0 * BITS, v[k]);
-    }
-  }
+  load_planes16<BITS, MODE, SERIAL>(p, desc + tc.slot * 16, sym0, nv > 0, v);
   if (MODE == kRowsShift && nv < 16) {  // other modes: T % 16 == 0
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -932,13 +999,15 @@ __device__ __forceinline__ void unpack_tile(const RowsParams& p, TileIndex ti,
   });
 }
 
-template <int BITS, int MODE>
+// ONEBLK as for for_rows16, SERIAL as for load_planes16; the host picks both
+// by launch size.
+template <int BITS, int MODE, bool ONEBLK, bool SERIAL>
 __global__ __launch_bounds__(kRowsThreads) void rows_unpack_kernel(RowsParams p) {
   __shared__ int64_t desc[kTilePlanes];
   for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     const TileIndex ti = split_tile(p, tile);
     load_descriptors(p, ti, desc);
-    unpack_tile<BITS, MODE>(p, ti, desc);
+    unpack_tile<BITS, MODE, false, ONEBLK, SERIAL>(p, ti, desc);
   }
 }
 
@@ -965,7 +1034,7 @@ __global__ __launch_bounds__(kRowsSplitWaves * 64) void rows_unpack_split_kernel
 // then restores its run as 16-token sub-tiles: expand, transpose, 16 row
 // stores each.  Needs T % (128 / b) == 0, so a run holds symbols either
 // throughout or not at all.
-template <int BITS, bool NT>
+template <int BITS, bool NT, bool ONEBLK>
 __device__ __forceinline__ void unpack_tile_wide(const RowsParams& p, TileIndex ti,
                                                  const int64_t* desc) {
   static_assert(BITS == 1 || BITS == 2 || BITS == 4, "wide runs are 16 bytes of 1, 2 or 4-bit symbols");
@@ -1011,8 +1080,7 @@ __device__ __forceinline__ void unpack_tile_wide(const RowsParams& p, TileIndex 
     }
     uint32_t o[16][4];
     transpose16(v, o);
-    // the cursor's waits: the one-block rows ran 2-4% slower here
-    for_rows16<false>(p, tc.half, t0, p.row_tokens - t0, [&](int j, int64_t row) {
+    for_rows16<ONEBLK>(p, tc.half, t0, p.row_tokens - t0, [&](int j, int64_t row) {
       const u32x4 x = {o[j][0], o[j][1], o[j][2], o[j][3]};
       __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(col + row * p.row_pitch));
     });
@@ -1023,13 +1091,13 @@ __device__ __forceinline__ void unpack_tile_wide(const RowsParams& p, TileIndex 
 // 16 planes stay in registers while the sub-tiles are restored.
 constexpr int kWideMaxWaves = 8;
 
-template <int BITS, bool NT>
+template <int BITS, bool NT, bool ONEBLK>
 __global__ __launch_bounds__(kWideMaxWaves * 64) void rows_unpack_wide_kernel(RowsParams p) {
   __shared__ int64_t desc[kTilePlanes];
   for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     const TileIndex ti = split_tile(p, tile);
     load_descriptors(p, ti, desc);
-    unpack_tile_wide<BITS, NT>(p, ti, desc);
+    unpack_tile_wide<BITS, NT, ONEBLK>(p, ti, desc);
   }
 }
 
@@ -1039,7 +1107,7 @@ __global__ __launch_bounds__(kWideMaxWaves * 64) void rows_unpack_wide_kernel(Ro
 // kBatchRequests tile offsets (a request with no tiles in a range has the next
 // request's offset, so the scan passes it).
 // Restores tile `tile` of a batched launch (slice `slice` of it with SPLIT).
-template <int BITS, int MODE, bool SPLIT, bool ONEBLK>
+template <int BITS, int MODE, bool SPLIT, bool ONEBLK, bool SERIAL>
 __device__ __forceinline__ void batch_tile(const RowsBatch& b, int64_t tile, int64_t* desc,
                                            int slice) {
   int r = 0;
@@ -1074,15 +1142,15 @@ __device__ __forceinline__ void batch_tile(const RowsBatch& b, int64_t tile, int
     else
       unpack_tile<BITS, kRowsAligned16Cached, SPLIT, ONEBLK>(p, ti, desc, slice);
   } else {
-    unpack_tile<BITS, MODE, SPLIT, ONEBLK>(p, ti, desc, slice);
+    unpack_tile<BITS, MODE, SPLIT, ONEBLK, SERIAL>(p, ti, desc, slice);
   }
 }
 
-template <int BITS, int MODE>
+template <int BITS, int MODE, bool ONEBLK, bool SERIAL>
 __global__ __launch_bounds__(kRowsThreads) void rows_unpack_batch_kernel(RowsBatch b) {
   __shared__ int64_t desc[kTilePlanes];
   for (int64_t tile = blockIdx.x; tile < b.common.ntiles; tile += gridDim.x)
-    batch_tile<BITS, MODE, false, false>(b, tile, desc, 0);
+    batch_tile<BITS, MODE, false, ONEBLK, SERIAL>(b, tile, desc, 0);
 }
 
 // The batched restore with each tile dispatched as 2^sh workgroups of
@@ -1093,7 +1161,8 @@ __global__ __launch_bounds__(kRowsSplitWaves * 64) void rows_unpack_batch_split_
   __shared__ int64_t desc[kTilePlanes];
   const int64_t slots = b.common.ntiles << sh;
   for (int64_t s = blockIdx.x; s < slots; s += gridDim.x)
-    batch_tile<BITS, MODE, true, ONEBLK>(b, s >> sh, desc, static_cast<int>(s & ((1 << sh) - 1)));
+    batch_tile<BITS, MODE, true, ONEBLK, false>(b, s >> sh, desc,
+                                               static_cast<int>(s & ((1 << sh) - 1)));
 }
 
 // Calls f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order.
@@ -1145,27 +1214,24 @@ __device__ __forceinline__ void store_chunk_part(uint8_t* dst, uint32_t c0, uint
 
 // Gathers a lane's 16 rows x 16 bytes (tokens t0 .. t0 + nv - 1 of its
 // 16-byte channel column) through the block table; missing rows read as 0.
+// ONEBLK as for for_rows16: without it the row loads are requested one after
+// another, which is faster only in launches of more than 12 waves per CU
+// (6 for the staged pack).
+template <bool ONEBLK>
 __device__ __forceinline__ void load_tile_rows(const RowsParams& p, const TileCoord& tc, int nv,
                                                uint32_t (&r)[16][4]) {
-  RowCursor rc;
-  cursor_init(p, tc.t0, rc);
   const uint8_t* col = p.rows + static_cast<int64_t>(tc.h) * p.head_pitch + tc.q * 16;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    r[j][0] = r[j][1] = r[j][2] = r[j][3] = 0;
-    if (j < nv) {
-      if (j > 0) cursor_next(p, rc);
-      const int64_t row = cursor_row(p, tc.half, rc);
-      if (row >= 0) {
-        const u32x4 x =
-            __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(col + row * p.row_pitch));
-        r[j][0] = x.x;
-        r[j][1] = x.y;
-        r[j][2] = x.z;
-        r[j][3] = x.w;
-      }
-    }
-  }
+  for (int j = 0; j < 16; ++j) r[j][0] = r[j][1] = r[j][2] = r[j][3] = 0;
+  if (nv <= 0) return;
+  for_rows16<ONEBLK>(p, tc.half, tc.t0, nv, [&](int j, int64_t row) {
+    const u32x4 x =
+        __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(col + row * p.row_pitch));
+    r[j][0] = x.x;
+    r[j][1] = x.y;
+    r[j][2] = x.z;
+    r[j][3] = x.w;
+  });
 }
 
 // 8-bit pack of planes off 128-byte lines (kRowsStaged8), staged through LDS.
@@ -1215,7 +1281,7 @@ __device__ __forceinline__ void store_region_chunk(uint8_t* line0, const uint8_t
 // Every wave of the workgroup runs this for every tile (no early exit: the
 // rounds hold barriers); lanes outside the tile's channels or tokens only
 // take part in the barriers.
-template <int WAVES>
+template <int WAVES, bool ONEBLK>
 __device__ __forceinline__ void pack_tile_staged8(const RowsParams& p, TileIndex ti,
                                                   const int64_t* desc, uint8_t* stage) {
   const TileCoord tc = tile_coord(p, ti);
@@ -1227,7 +1293,7 @@ __device__ __forceinline__ void pack_tile_staged8(const RowsParams& p, TileIndex
   const int nv = run_ok ? static_cast<int>(p.T - tc.t0 < 16 ? p.T - tc.t0 : 16) : 0;
 
   uint32_t r[16][4];
-  load_tile_rows(p, tc, nv, r);
+  load_tile_rows<ONEBLK>(p, tc, nv, r);
   uint32_t v[16][4];
   transpose16(r, v);
 
@@ -1261,7 +1327,7 @@ __device__ __forceinline__ void pack_tile_staged8(const RowsParams& p, TileIndex
   });
 }
 
-template <int BITS, int MODE>
+template <int BITS, int MODE, bool ONEBLK>
 __device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
                                           const int64_t* desc) {
   const TileCoord tc = tile_coord(p, ti);
@@ -1269,7 +1335,7 @@ __device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
   const int nv = static_cast<int>(p.T - tc.t0 < 16 ? p.T - tc.t0 : 16);
 
   uint32_t r[16][4];
-  load_tile_rows(p, tc, nv, r);
+  load_tile_rows<ONEBLK>(p, tc, nv, r);
   uint32_t v[16][4];
   transpose16(r, v);
 
@@ -1287,27 +1353,27 @@ __device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
   }
 }
 
-template <int BITS, int MODE>
+template <int BITS, int MODE, bool ONEBLK>
 __global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
   __shared__ int64_t desc[kTilePlanes];
   for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     const TileIndex ti = split_tile(p, tile);
     load_descriptors(p, ti, desc);
-    pack_tile<BITS, MODE>(p, ti, desc);
+    pack_tile<BITS, MODE, ONEBLK>(p, ti, desc);
   }
 }
 
 // The 8-bit pack off 128-byte lines (kRowsStaged8), for workgroups of WAVES
 // waves (p.waves == WAVES): LDS in proportion, so that the smaller workgroups
 // of short launches still share a CU.
-template <int WAVES>
+template <int WAVES, bool ONEBLK>
 __global__ __launch_bounds__(WAVES * 64) void rows_pack_staged8_kernel(RowsParams p) {
   __shared__ int64_t desc[kRowsWq * kWavePlanes];
   __shared__ __align__(16) uint8_t stage[2 * stage_round_bytes(WAVES)];
   for (int64_t tile = blockIdx.x; tile < p.ntiles; tile += gridDim.x) {
     const TileIndex ti = split_tile(p, tile);
     load_descriptors(p, ti, desc);
-    pack_tile_staged8<WAVES>(p, ti, desc, stage);
+    pack_tile_staged8<WAVES, ONEBLK>(p, ti, desc, stage);
   }
 }
 
@@ -1598,6 +1664,54 @@ void set_batch_grid(RowsBatch& b, int64_t H, int64_t C) {
   p.ntiles = tile0;
 }
 
+// Average waves per CU over a launch of `ntiles` workgroups of `waves` waves,
+// at most the 16 a CU holds at once.
+double waves_per_cu(int64_t ntiles, int waves) {
+  const double w = static_cast<double>(ntiles) * waves / device_cu_count();
+  return w < 16.0 ? w : 16.0;
+}
+
+// Row order of the whole-tile row kernels by launch size (waves per CU).
+// One-block rows (for_rows16) for restores and staged packs up to 6 waves per
+// CU (4096 tokens of Llama-3-8B: 9.6 -> 8.0 us; 8192 tokens: 14.0 -> 14.6, so
+// not above), for the other packs up to 12 (4096 tokens: 2.07 -> 4.03 TB/s;
+// 12288: 4.50 -> 4.74; 16384 tokens at 16: 5.07 -> 4.83).  Serial plane loads
+// (load_planes16) for b = 7, 8 shift restores above 12 waves per CU.
+constexpr double kOneBlockWaves = 6;
+constexpr double kOneBlockPackWaves = 12;
+constexpr double kSerialLoadWaves = 12;
+
+bool one_block_rows(const RowsParams& p) { return !p.block_ids || (p.bs & 15) == 0; }
+
+// A batched restore: split (sh > 0) into 4-wave slices, or whole-tile
+// workgroups with the row order of launch_unpack_tiles.
+template <int BITS, int MODE>
+void launch_batch_tiles(dim3 grid, dim3 block, hipStream_t stream, const RowsBatch& b, int sh,
+                        bool oneblk, bool serial) {
+  if (sh > 0) {
+    if (oneblk)
+      hipLaunchKernelGGL((rows_unpack_batch_split_kernel<BITS, MODE, true>), grid, block, 0,
+                         stream, b, sh);
+    else
+      hipLaunchKernelGGL((rows_unpack_batch_split_kernel<BITS, MODE, false>), grid, block, 0,
+                         stream, b, sh);
+    return;
+  }
+  if constexpr (MODE == kRowsShift && BITS >= 7) {
+    if (serial && !oneblk) {
+      hipLaunchKernelGGL((rows_unpack_batch_kernel<BITS, MODE, false, true>), grid, block, 0,
+                         stream, b);
+      return;
+    }
+  }
+  if (oneblk)
+    hipLaunchKernelGGL((rows_unpack_batch_kernel<BITS, MODE, true, false>), grid, block, 0,
+                       stream, b);
+  else
+    hipLaunchKernelGGL((rows_unpack_batch_kernel<BITS, MODE, false, false>), grid, block, 0,
+                       stream, b);
+}
+
 int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream) {
   if (b.common.ntiles <= 0) return ORIGAMI_OK;
   // At least kRowsSplitTiles tiles per CU: each tile as 4-wave workgroups,
@@ -1607,36 +1721,29 @@ int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream
       b.common.ntiles >= kRowsSplitTiles * static_cast<int64_t>(device_cu_count()))
     while ((kRowsSplitWaves << sh) < b.common.waves) ++sh;
   const bool split = sh > 0;
-  bool oneblk = true;  // as for_rows16 needs it, for every request
+  bool rows1 = true;  // one-block rows (for_rows16) possible for every request
   for (int r = 0; r < b.nreq; ++r)
-    if (b.req[r].block_ids && (b.common.bs & 15) != 0) oneblk = false;
+    if (b.req[r].block_ids && (b.common.bs & 15) != 0) rows1 = false;
+  // whole-tile workgroups: the single-request rules by launch size
+  const double wpc = waves_per_cu(b.common.ntiles, b.common.waves);
+  const bool oneblk = rows1 && (split || wpc <= kOneBlockWaves);
+  const bool serial = !split && wpc > kSerialLoadWaves;
   int64_t blocks = b.common.ntiles << sh;
   if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
   if (blocks > INT32_MAX) blocks = INT32_MAX;
   const dim3 grid(static_cast<unsigned>(blocks)),
       block(static_cast<unsigned>(64 * (split ? kRowsSplitWaves : b.common.waves)));
-#define ORIGAMI_BATCH_LAUNCH(B, M)                                                              \
-  do {                                                                                          \
-    if (split && oneblk)                                                                        \
-      hipLaunchKernelGGL((rows_unpack_batch_split_kernel<B, M, true>), grid, block, 0, stream, b, \
-                         sh);                                                                   \
-    else if (split)                                                                             \
-      hipLaunchKernelGGL((rows_unpack_batch_split_kernel<B, M, false>), grid, block, 0, stream,   \
-                         b, sh);                                                                \
-    else                                                                                        \
-      hipLaunchKernelGGL((rows_unpack_batch_kernel<B, M>), grid, block, 0, stream, b);          \
-  } while (0)
   if (bits == 8 && mode == kRowsAligned16) {
-    ORIGAMI_BATCH_LAUNCH(8, kRowsAligned16);
+    launch_batch_tiles<8, kRowsAligned16>(grid, block, stream, b, sh, oneblk, serial);
     return check_launch("rows_unpack_batch_kernel");
   }
   const bool window = mode == kRowsWindow;
-#define ORIGAMI_BATCH_CASE(B)                  \
-  case B:                                      \
-    if (window)                                \
-      ORIGAMI_BATCH_LAUNCH(B, kRowsWindow);    \
-    else                                       \
-      ORIGAMI_BATCH_LAUNCH(B, kRowsShift);     \
+#define ORIGAMI_BATCH_CASE(B)                                                          \
+  case B:                                                                              \
+    if (window)                                                                        \
+      launch_batch_tiles<B, kRowsWindow>(grid, block, stream, b, sh, oneblk, serial);  \
+    else                                                                               \
+      launch_batch_tiles<B, kRowsShift>(grid, block, stream, b, sh, oneblk, serial);   \
     break;
   switch (bits) {
     ORIGAMI_BATCH_CASE(1)
@@ -1651,7 +1758,6 @@ int launch_rows_batch(const RowsBatch& b, int bits, int mode, hipStream_t stream
       return fail(ORIGAMI_ERR_INVALID, "Origami CUDA bitpack supports only 1..8 bit symbols");
   }
 #undef ORIGAMI_BATCH_CASE
-#undef ORIGAMI_BATCH_LAUNCH
   return check_launch("rows_unpack_batch_kernel");
 }
 
@@ -1717,6 +1823,52 @@ int pack_mode(const PlanInfo& info, const RowsParams& p, int64_t T) {
 constexpr int kStagedWq = 1;
 
 template <int BITS, int MODE>
+void launch_unpack_tiles(dim3 grid, dim3 block, hipStream_t stream, const RowsParams& p,
+                         bool oneblk, bool serial) {
+  if constexpr (MODE == kRowsShift && BITS >= 7) {
+    if (serial && !oneblk) {
+      hipLaunchKernelGGL((rows_unpack_kernel<BITS, MODE, false, true>), grid, block, 0, stream, p);
+      return;
+    }
+  }
+  if (oneblk)
+    hipLaunchKernelGGL((rows_unpack_kernel<BITS, MODE, true, false>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((rows_unpack_kernel<BITS, MODE, false, false>), grid, block, 0, stream, p);
+}
+
+template <int BITS, int MODE>
+void launch_pack_tiles(dim3 grid, dim3 block, hipStream_t stream, const RowsParams& p,
+                       bool oneblk) {
+  if (oneblk)
+    hipLaunchKernelGGL((rows_pack_kernel<BITS, MODE, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((rows_pack_kernel<BITS, MODE, false>), grid, block, 0, stream, p);
+}
+
+template <int WAVES>
+void launch_staged_tiles(dim3 grid, dim3 block, hipStream_t stream, const RowsParams& p,
+                         bool oneblk) {
+  if (oneblk)
+    hipLaunchKernelGGL((rows_pack_staged8_kernel<WAVES, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((rows_pack_staged8_kernel<WAVES, false>), grid, block, 0, stream, p);
+}
+
+template <int BITS>
+void launch_wide_tiles(dim3 grid, dim3 block, hipStream_t stream, const RowsParams& p, bool nt,
+                       bool oneblk) {
+  if (nt && oneblk)
+    hipLaunchKernelGGL((rows_unpack_wide_kernel<BITS, true, true>), grid, block, 0, stream, p);
+  else if (nt)
+    hipLaunchKernelGGL((rows_unpack_wide_kernel<BITS, true, false>), grid, block, 0, stream, p);
+  else if (oneblk)
+    hipLaunchKernelGGL((rows_unpack_wide_kernel<BITS, false, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((rows_unpack_wide_kernel<BITS, false, false>), grid, block, 0, stream, p);
+}
+
+template <int BITS, int MODE>
 int launch_split(dim3 grid, dim3 block, hipStream_t stream, const RowsParams& p, int sh,
                  bool oneblk) {
   if (oneblk)
@@ -1768,77 +1920,73 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
   // partial token tiles last: restore 32784 tokens 64.0 -> 61.4 us, 49216
   // tokens 96.8 -> 94.8 us; the pack ran 2-5% slower that way
   if (pack) p.partial_last = 0;
-  if (mode == kRowsWide || mode == kRowsWideCached) {
-    if (pack || p.waves > kWideMaxWaves)
-      return fail(ORIGAMI_ERR_INVALID, "wide rows mode is a restore of at most 8-wave tiles");
-    int64_t blocks = p.ntiles;
-    if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
-    if (blocks > INT32_MAX) blocks = INT32_MAX;
-    const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(64 * p.waves));
-    const bool nt = mode == kRowsWide;
-#define ORIGAMI_WIDE_CASE(B)                                                                \
-  case B:                                                                                   \
-    if (nt)                                                                                 \
-      hipLaunchKernelGGL((rows_unpack_wide_kernel<B, true>), grid, block, 0, stream, p);    \
-    else                                                                                    \
-      hipLaunchKernelGGL((rows_unpack_wide_kernel<B, false>), grid, block, 0, stream, p);   \
-    break;
-    switch (bits) {
-      ORIGAMI_WIDE_CASE(1)
-      ORIGAMI_WIDE_CASE(2)
-      ORIGAMI_WIDE_CASE(4)
-      default:
-        return fail(ORIGAMI_ERR_INVALID, "wide rows mode takes 1, 2 or 4-bit symbols");
-    }
-#undef ORIGAMI_WIDE_CASE
-    return check_launch("rows_unpack_wide_kernel");
-  }
-  if (!pack && p.waves > kRowsSplitWaves &&
+  if (!pack && mode != kRowsWide && mode != kRowsWideCached && p.waves > kRowsSplitWaves &&
       p.ntiles >= kRowsSplitTiles * static_cast<int64_t>(device_cu_count()))
     return launch_rows_split(p, bits, mode, stream);
   int64_t blocks = p.ntiles;
   if (g_rows_grid_limit > 0 && blocks > g_rows_grid_limit) blocks = g_rows_grid_limit;
   if (blocks > INT32_MAX) blocks = INT32_MAX;
   const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(64 * p.waves));
+  const double wpc = waves_per_cu(p.ntiles, p.waves);
+  const bool staged = mode == kRowsStaged8;
+  const bool oneblk =
+      one_block_rows(p) && wpc <= (pack && !staged ? kOneBlockPackWaves : kOneBlockWaves);
+  const bool serial = wpc > kSerialLoadWaves;
+  if (mode == kRowsWide || mode == kRowsWideCached) {
+    if (pack || p.waves > kWideMaxWaves)
+      return fail(ORIGAMI_ERR_INVALID, "wide rows mode is a restore of at most 8-wave tiles");
+    const bool nt = mode == kRowsWide;
+    switch (bits) {
+      case 1:
+        launch_wide_tiles<1>(grid, block, stream, p, nt, oneblk);
+        break;
+      case 2:
+        launch_wide_tiles<2>(grid, block, stream, p, nt, oneblk);
+        break;
+      case 4:
+        launch_wide_tiles<4>(grid, block, stream, p, nt, oneblk);
+        break;
+      default:
+        return fail(ORIGAMI_ERR_INVALID, "wide rows mode takes 1, 2 or 4-bit symbols");
+    }
+    return check_launch("rows_unpack_wide_kernel");
+  }
   if (bits == 8 && mode == kRowsAligned16) {
     if (pack)
-      hipLaunchKernelGGL((rows_pack_kernel<8, kRowsAligned16>), grid, block, 0, stream, p);
+      launch_pack_tiles<8, kRowsAligned16>(grid, block, stream, p, oneblk);
     else
-      hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsAligned16>), grid, block, 0, stream, p);
+      launch_unpack_tiles<8, kRowsAligned16>(grid, block, stream, p, oneblk, serial);
     return check_launch(pack ? "rows_pack_kernel" : "rows_unpack_kernel");
   }
-  if (pack && bits == 8 && mode != kRowsStaged8)  // pack_mode: aligned16 or staged
+  if (pack && bits == 8 && !staged)  // pack_mode: aligned16 or staged
     return fail(ORIGAMI_ERR_INVALID, "8-bit rows pack modes are aligned16 and staged");
   if (bits == 8 && mode == kRowsAligned16Cached) {
-    hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsAligned16Cached>), grid, block, 0, stream, p);
+    launch_unpack_tiles<8, kRowsAligned16Cached>(grid, block, stream, p, oneblk, serial);
     return check_launch("rows_unpack_kernel");
   }
-  if (mode == kRowsStaged8) {
+  if (staged) {
     if (!pack || bits != 8) return fail(ORIGAMI_ERR_INVALID, "staged rows mode is the 8-bit pack");
     if (p.waves == 16)
-      hipLaunchKernelGGL(rows_pack_staged8_kernel<16>, grid, block, 0, stream, p);
+      launch_staged_tiles<16>(grid, block, stream, p, oneblk);
     else if (p.waves == 8)
-      hipLaunchKernelGGL(rows_pack_staged8_kernel<8>, grid, block, 0, stream, p);
+      launch_staged_tiles<8>(grid, block, stream, p, oneblk);
     else if (p.waves == 4)
-      hipLaunchKernelGGL(rows_pack_staged8_kernel<4>, grid, block, 0, stream, p);
+      launch_staged_tiles<4>(grid, block, stream, p, oneblk);
     else
       return fail(ORIGAMI_ERR_INVALID, "staged pack workgroups have 4, 8 or 16 waves");
     return check_launch("rows_pack_staged8_kernel");
   }
   const bool window = mode == kRowsWindow;
-#define ORIGAMI_ROWS_CASE(B)                                                                  \
-  case B:                                                                                     \
-    if (pack) {                                                                               \
-      if (window)                                                                             \
-        hipLaunchKernelGGL((rows_pack_kernel<B, kRowsWindow>), grid, block, 0, stream, p);    \
-      else                                                                                    \
-        hipLaunchKernelGGL((rows_pack_kernel<B, kRowsBytes>), grid, block, 0, stream, p);     \
-    } else {                                                                                  \
-      if (window)                                                                             \
-        hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsWindow>), grid, block, 0, stream, p);  \
-      else                                                                                    \
-        hipLaunchKernelGGL((rows_unpack_kernel<B, kRowsShift>), grid, block, 0, stream, p);   \
-    }                                                                                         \
+#define ORIGAMI_ROWS_CASE(B)                                                          \
+  case B:                                                                             \
+    if (pack && window)                                                               \
+      launch_pack_tiles<B, kRowsWindow>(grid, block, stream, p, oneblk);              \
+    else if (pack)                                                                    \
+      launch_pack_tiles<B, kRowsBytes>(grid, block, stream, p, oneblk);               \
+    else if (window)                                                                  \
+      launch_unpack_tiles<B, kRowsWindow>(grid, block, stream, p, oneblk, serial);    \
+    else                                                                              \
+      launch_unpack_tiles<B, kRowsShift>(grid, block, stream, p, oneblk, serial);     \
     break;
   switch (bits) {
     ORIGAMI_ROWS_CASE(1)
@@ -1850,9 +1998,9 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
     ORIGAMI_ROWS_CASE(7)
     case 8:  // restore only: the 8-bit pack is aligned16 or staged
       if (window)
-        hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsWindow>), grid, block, 0, stream, p);
+        launch_unpack_tiles<8, kRowsWindow>(grid, block, stream, p, oneblk, serial);
       else
-        hipLaunchKernelGGL((rows_unpack_kernel<8, kRowsShift>), grid, block, 0, stream, p);
+        launch_unpack_tiles<8, kRowsShift>(grid, block, stream, p, oneblk, serial);
       break;
     default:
       return fail(ORIGAMI_ERR_INVALID, "Origami CUDA bitpack supports only 1..8 bit symbols");

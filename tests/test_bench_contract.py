@@ -67,7 +67,7 @@ def test_committed_traffic_is_the_profiles_figure():
                               bits=8)
     line = next(l for l in (REPO / "profiles" / "rows_unpack_llama3_8b_32k.txt")
                 .read_text().splitlines()
-                if l.startswith("traffic_bytes_per_launch rows_unpack_kernel<8, 2>:"))
+                if l.startswith("traffic_bytes_per_launch rows_unpack_kernel<8, 2, false, false>:"))
     assert bench.committed_traffic(args) == int(line.split(":")[1].split()[0])
     # a workload the summary does not cover reports no traffic
     args.tokens = 4096

@@ -145,7 +145,31 @@ def test_large_single_request_split_launch(cuda_device, T, bits, bs):
     oracle's unpack + scatter of the oracle's pack.  With 16-token blocks a
     lane's 16 rows lie in one block; 24- and 8-token blocks take the
     row-by-row walk of the block table."""
-    dev, H, C = cuda_device, 8, 256
+    _restore_random_layer(cuda_device, T, bits, bs)
+
+
+@pytest.mark.parametrize("T,bits,bs", [
+    (32753, 7, 16),   # 16-wave tiles, 16 waves per CU: plane loads one plane at a time
+    (32753, 8, 24),   # the same with the block-table walk
+    (15000, 8, 16),   # 4-wave tiles, ~15 waves per CU: serial plane loads
+    (8200, 8, 16),    # ~8 waves per CU: every plane load in flight, block-table walk
+    (4100, 7, 16),    # ~4 waves per CU: one block per lane
+    (4100, 5, 8),     # the same launch size with 8-token blocks
+])
+def test_restore_orders_by_launch_size(cuda_device, T, bits, bs):
+    """Whole-tile restores whose launch size picks the order of plane loads
+    and row stores (the results must not depend on it)."""
+    _restore_random_layer(cuda_device, T, bits, bs)
+
+
+def test_batch_serial_plane_loads(cuda_device):
+    """A batch of four ragged ~8000-token requests in 16-wave tiles (512
+    tiles, one launch with 16 waves per CU)."""
+    _run(cuda_device, 8, 128, torch.bfloat16, [8001, 7999, 8003, 7995], 6, False, batch=True)
+
+
+def _restore_random_layer(dev, T, bits, bs):
+    H, C = 8, 256
     rng = np.random.default_rng(T + bits)
     plan = plan_head_channel_chunks(layer_index=0, num_heads=H, head_dim=C, token_count=2 * T,
                                     bytes_per_symbol=1, min_bytes=1 << 20,
