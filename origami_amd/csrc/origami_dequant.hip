@@ -486,23 +486,39 @@ __device__ __forceinline__ void kivi_tile(
   const int64_t h = c0 / p.D, d0 = c0 - h * p.D;  // D % 8 == 0: one head
   const int64_t plane0 = half == 0 ? d0 * p.H + h : c0;
   const int64_t pstep = (half == 0 ? p.H : 1) * p.body * SBITS;
-  int64_t P = hs.bit_bias + (plane0 * p.body + bt0) * SBITS;
-  uint32_t u[8][NU];
+  const int64_t P0 = hs.bit_bias + (plane0 * p.body + bt0) * SBITS;
+  // Every plane's dwords are requested before any funnel shift: with the
+  // shift next to each plane's loads, the compiler waited for each plane's
+  // data before requesting the next plane's.  A run whose dwords would pass
+  // the end of the stream is read again dword by dword afterwards.
+  uint32_t w[8][NU + 1];
+  uint32_t tail = 0;     // bit i: plane i's dwords pass the end of the stream
+  uint32_t shp[2] = {};  // byte i & 3 of shp[i >> 2]: plane i's funnel shift
 #pragma unroll
-  for (int i = 0; i < 8; ++i, P += pstep) {
+  for (int i = 0; i < 8; ++i) {
+    const int64_t P = P0 + i * pstep;
     const int64_t byte0 = (P >> 5) * 4;
-    const uint32_t sh = static_cast<uint32_t>(P & 31);
-    uint32_t w[NU + 1];
+    shp[i >> 2] |= static_cast<uint32_t>(P & 31) << (8 * (i & 3));
     if (byte0 + 4 * (NU + 1) <= hs.sbytes) {
       const uint32_t* src = reinterpret_cast<const uint32_t*>(hs.sbase + byte0);
 #pragma unroll
-      for (int k = 0; k <= NU; ++k) w[k] = src[k];
+      for (int k = 0; k <= NU; ++k) w[i][k] = src[k];
     } else {
+      tail |= 1u << i;
+    }
+  }
+  uint32_t u[8][NU];
 #pragma unroll
-      for (int k = 0; k <= NU; ++k) w[k] = load_dword_guarded(hs.sbase, byte0 + 4 * k, hs.sbytes);
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t sh = (shp[i >> 2] >> (8 * (i & 3))) & 31u;
+    if (tail & (1u << i)) {
+      const int64_t byte0 = ((P0 + i * pstep) >> 5) * 4;
+#pragma unroll
+      for (int k = 0; k <= NU; ++k)
+        w[i][k] = load_dword_guarded(hs.sbase, byte0 + 4 * k, hs.sbytes);
     }
 #pragma unroll
-    for (int k = 0; k < NU; ++k) u[i][k] = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);
+    for (int k = 0; k < NU; ++k) u[i][k] = __builtin_amdgcn_alignbit(w[i][k + 1], w[i][k], sh);
   }
 
   const int nj = static_cast<int>(min<int64_t>(LT, p.body - bt0));
