@@ -453,6 +453,9 @@ enum RowsMode : int {
   // non-temporal when every group's 8 runs are one 128-byte line
   kRowsWide = 7,
   kRowsWideCached = 8,
+  // pack, b < 8, planes not all on bytes (T * b % 8 != 0 or unaligned chunk
+  // planes): runs start at any bit and are ORed into the cleared stream
+  kRowsBits = 9,
 };
 
 struct RowsParams {
@@ -1327,6 +1330,49 @@ __device__ __forceinline__ void pack_tile_staged8(const RowsParams& p, TileIndex
   });
 }
 
+// Writes the low `nbits` bits (> 0) of u[] into the stream at bit P
+// (kRowsBits).  The 8 lanes of a group hold consecutive runs of one plane,
+// lane i at P0 + 16 b i, and the group's bits are [P0, Pend).  A dword wholly
+// inside that range is stored by the lane holding its first bit, with the
+// next lane's leading bits merged in (a dword spans at most two runs for
+// b >= 2).  The dwords at the range's ends are shared with other groups
+// (other waves, tiles or planes): their bits go in with atomic ORs into the
+// stream, which the launch clears first.  Below b = 5 every dword does: the
+// plain stores then cost more than the ORs they replace (32753 tokens, GB/s
+// with / without the merge: b = 7 719 / 469, 6 721 / 581, 5 654 / 618,
+// 3 656 / 851, 2 937 / 1235).  Every lane of the group with symbols must call
+// this (the merge reads the next lane's first dword); no bit outside the run
+// is set and no dword past its last bit is touched.
+template <int BITS>
+__device__ __forceinline__ void put_run_bits(uint8_t* stream, int64_t P, const uint32_t* u,
+                                             int nbits, int64_t P0, int64_t Pend) {
+  constexpr int NU = (16 * BITS + 31) / 32;
+  const int64_t D0 = P >> 5;
+  uint32_t* const base = reinterpret_cast<uint32_t*>(stream) + D0;
+  const uint32_t s = static_cast<uint32_t>(P & 31);
+  const int last = static_cast<int>((s + nbits - 1) >> 5);  // last dword index touched
+  uint32_t g[NU + 1];
+#pragma unroll
+  for (int i = 0; i <= NU; ++i) {
+    const uint64_t hi = i < NU ? u[i] : 0u, lo = i > 0 ? u[i - 1] : 0u;
+    g[i] = static_cast<uint32_t>(((hi << 32) | lo) >> (32 - s));
+  }
+  const uint32_t next0 = __shfl_down(g[0], 1, 8);  // the next run's first dword
+  const int64_t Pn = P + 16 * BITS;
+#pragma unroll
+  for (int i = 0; i <= NU; ++i) {
+    if (i > last) break;
+    const int64_t D = D0 + i;
+    const bool inside = BITS >= 5 && 32 * D >= P0 && 32 * D + 32 <= Pend;
+    if (!inside) {
+      if (g[i] != 0) atomicOr(base + i, g[i]);
+    } else if (32 * D >= P) {  // else the previous lane holds its first bit
+      const bool merge = (Pn & 31) != 0 && (Pn >> 5) == D;
+      base[i] = merge ? (g[i] | next0) : g[i];
+    }
+  }
+}
+
 template <int BITS, int MODE, bool ONEBLK>
 __device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
                                           const int64_t* desc) {
@@ -1346,10 +1392,18 @@ __device__ __forceinline__ void pack_tile(const RowsParams& p, TileIndex ti,
   for (int k = 0; k < 16; ++k) {
     const int64_t d = desc[tc.slot * 16 + k];
     if (d < 0) continue;
-    const int64_t P = d + p.bit_bias + sym0 * BITS;  // byte aligned by plan
+    const int64_t P = d + p.bit_bias + sym0 * BITS;  // byte aligned unless kRowsBits
     uint32_t u[NU > 4 ? NU : 4];
     compress16<BITS>(v[k], u);
-    store_stream<BITS, MODE>(p.stream + (P >> 3), u, nbytes);
+    if constexpr (MODE == kRowsBits) {
+      // the group's runs: 8 lanes from token t0g, those below T hold symbols
+      const int64_t t0g = tc.t0 - static_cast<int64_t>(threadIdx.x & 7) * kSegTokens;
+      const int64_t ng = p.T - t0g < 8 * kSegTokens ? p.T - t0g : 8 * kSegTokens;
+      const int64_t P0 = P - (tc.t0 - t0g) * BITS;
+      put_run_bits<BITS>(p.stream, P, u, nv * BITS, P0, P0 + ng * BITS);
+    } else {
+      store_stream<BITS, MODE>(p.stream + (P >> 3), u, nbytes);
+    }
   }
 }
 
@@ -1811,6 +1865,7 @@ void set_restore_grid(RowsParams& p, int mode, int bits, int64_t H, int64_t C,
 // non-temporal stores even when the V half is not: 3874 against 3608 staged
 // at 32832 tokens.
 int pack_mode(const PlanInfo& info, const RowsParams& p, int64_t T) {
+  if (info.bits < 8 && (!info.byte_aligned || (T * info.bits) % 8 != 0)) return kRowsBits;
   const int mode = rows_mode(info, p, T, true);
   if (info.bits == 8 && mode != kRowsAligned16) return kRowsStaged8;
   return mode;
@@ -1976,11 +2031,19 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
       return fail(ORIGAMI_ERR_INVALID, "staged pack workgroups have 4, 8 or 16 waves");
     return check_launch("rows_pack_staged8_kernel");
   }
+  if (mode == kRowsBits) {
+    if (!pack || bits >= 8) return fail(ORIGAMI_ERR_INVALID, "bit rows mode is a sub-byte pack");
+    // the runs are ORed in: clear the caller's stream bytes first
+    const int64_t lead = p.bit_bias >> 3;
+    if (int rc = launch_fill_zero(p.stream + lead, p.stream_bytes - lead, stream)) return rc;
+  }
   const bool window = mode == kRowsWindow;
 #define ORIGAMI_ROWS_CASE(B)                                                          \
   case B:                                                                             \
     if (pack && window)                                                               \
       launch_pack_tiles<B, kRowsWindow>(grid, block, stream, p, oneblk);              \
+    else if (pack && mode == kRowsBits)                                               \
+      launch_pack_tiles<B, kRowsBits>(grid, block, stream, p, oneblk);                \
     else if (pack)                                                                    \
       launch_pack_tiles<B, kRowsBytes>(grid, block, stream, p, oneblk);               \
     else if (window)                                                                  \
@@ -2349,7 +2412,7 @@ int origami_pack_canonical_storage_chunks(
   if (rc) return rc;
 
   if (rows_layout && plan->has_table && plan->info.regular && plan->info.bits != 0 &&
-      plan->info.byte_aligned && (T * plan->info.bits) % 8 == 0) {
+      (plan->info.bits < 8 || (plan->info.byte_aligned && (T * plan->info.bits) % 8 == 0))) {
     RowsParams p{};
     set_stream(p, flat_chunks, flat_bytes);
     if (int rc2 = set_planes(p, plan)) return rc2;
@@ -2605,9 +2668,9 @@ int origami_pack_canonical_from_kv_cache(
                 head_bytes, true, &plan);
   if (rc) return rc;
   if (!plan->has_table || !plan->info.regular || plan->info.bits == 0 ||
-      !plan->info.byte_aligned || (tokens * plan->info.bits) % 8 != 0)
+      (plan->info.bits == 8 && !plan->info.byte_aligned))
     return fail(ORIGAMI_ERR_UNSUPPORTED,
-                "fused save needs regular byte-aligned planes with one bit width");
+                "fused save needs regular planes with one bit width");
   RowsParams p{};
   set_stream(p, flat_chunks, flat_bytes);
   if (int rc2 = set_planes(p, plan)) return rc2;
