@@ -1638,7 +1638,7 @@ int device_cu_count() {
 // workgroups per CU over `nhalf` halves of `tile_tokens_total` tokens.
 void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_total,
                    int64_t nhalf, int wq_max = kRowsWq, int seg_tokens = kSegTokens,
-                   int max_waves = kRowsMaxWaves) {
+                   int max_waves = kRowsMaxWaves, int64_t want_tiles = 0) {
   if (H > 1 && p.head_pitch == C) {
     C *= H;
     H = 1;
@@ -1648,7 +1648,7 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
   p.nq = static_cast<int32_t>(C / 16);
   const int nqg = (p.nq + kLaneGroups - 1) / kLaneGroups;
   const int64_t segs = (tile_tokens_total + seg_tokens - 1) / seg_tokens;
-  const int64_t want = 2 * static_cast<int64_t>(device_cu_count());
+  const int64_t want = want_tiles > 0 ? want_tiles : 2 * static_cast<int64_t>(device_cu_count());
   for (int waves = max_waves;; waves /= 2) {
     const int wq_cap = std::min(waves == kRowsMaxWaves ? kRowsWq : 2, wq_max);
     int wq = 1;
@@ -1876,6 +1876,20 @@ int pack_mode(const PlanInfo& info, const RowsParams& p, int64_t T) {
 // with the neighbouring tiles (3766 GB/s at 32753 tokens, against 3436 for
 // 256 x 1024 tiles).
 constexpr int kStagedWq = 1;
+
+// Workgroup grid of a pack in `mode`.  The staged pack takes the largest
+// workgroups that still give half a tile per CU (the rows kernels want two):
+// its LDS rounds and barriers favour fewer, larger tiles.  GB/s with 4-, 8-
+// and 16-wave workgroups: 4100 tokens 1550 / 1649 / 1375, 8200 tokens 2320 /
+// 2315 / 2482, 15000 tokens 3235 / 3565 / 3824; at 2053 tokens 4-wave tiles
+// stay fastest (955 against 901 / 699).
+void set_pack_grid(RowsParams& p, int mode, int64_t H, int64_t C, int64_t T, int64_t nhalf) {
+  if (mode == kRowsStaged8)
+    set_grid_dims(p, H, C, T, nhalf, kStagedWq, kSegTokens, kRowsMaxWaves,
+                  std::max<int64_t>(1, device_cu_count() / 2));
+  else
+    set_grid_dims(p, H, C, T, nhalf);
+}
 
 template <int BITS, int MODE>
 void launch_unpack_tiles(dim3 grid, dim3 block, hipStream_t stream, const RowsParams& p,
@@ -2423,7 +2437,7 @@ int origami_pack_canonical_storage_chunks(
     p.head_pitch = st.head;
     p.bs = T;
     const int mode = pack_mode(plan->info, p, T);
-    set_grid_dims(p, H, C, T, 1, mode == kRowsStaged8 ? kStagedWq : kRowsWq);
+    set_pack_grid(p, mode, H, C, T, 1);
     return launch_rows(true, p, 1, plan->info.bits, mode, stream);
   }
 
@@ -2685,7 +2699,7 @@ int origami_pack_canonical_from_kv_cache(
   p.blk_stride = blk_stride;
   p.half_stride = half_stride;
   const int mode = pack_mode(plan->info, p, tokens);
-  set_grid_dims(p, num_heads, head_bytes, tokens, 2, mode == kRowsStaged8 ? kStagedWq : kRowsWq);
+  set_pack_grid(p, mode, num_heads, head_bytes, tokens, 2);
   return launch_rows(true, p, 2, plan->info.bits, mode, stream);
 }
 

@@ -43,8 +43,9 @@ def _oracle_threads():
     49216,   # planes on lines, V half off, partial last tile
     3088,    # small: 4-wave tiles, partial last tile
     32753,   # odd: runs at any byte; staged pack in 16-wave tiles
-    16383,   # odd: staged pack in 8-wave tiles
-    4100,    # staged pack in 4-wave tiles, 4-token last tile
+    16383,   # odd: staged pack in 16-wave tiles, one per CU
+    4100,    # staged pack in 8-wave tiles, 4-token last tile
+    2053,    # staged pack in 4-wave tiles
 ])
 @pytest.mark.parametrize("blocks_first", [False, True])
 def test_byte_planes_off_lines(cuda_device, T, blocks_first):
