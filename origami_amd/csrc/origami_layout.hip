@@ -1648,23 +1648,40 @@ void set_grid_dims(RowsParams& p, int64_t H, int64_t C, int64_t tile_tokens_tota
   p.nq = static_cast<int32_t>(C / 16);
   const int nqg = (p.nq + kLaneGroups - 1) / kLaneGroups;
   const int64_t segs = (tile_tokens_total + seg_tokens - 1) / seg_tokens;
-  const int64_t want = want_tiles > 0 ? want_tiles : 2 * static_cast<int64_t>(device_cu_count());
-  for (int waves = max_waves;; waves /= 2) {
+  const int64_t cus = device_cu_count();
+  const int64_t want = want_tiles > 0 ? want_tiles : 2 * cus;
+  // tiles of a `waves`-wave workgroup shape (sets the shape fields of p)
+  auto shape = [&](int waves) {
     const int wq_cap = std::min(waves == kRowsMaxWaves ? kRowsWq : 2, wq_max);
     int wq = 1;
-    while (wq < wq_cap && wq * 2 <= nqg) wq *= 2;
+    while (wq < wq_cap && wq * 2 <= nqg && wq * 2 <= waves) wq *= 2;
     p.waves = waves;
     p.wq = wq;
     p.ws = waves / wq;
     p.nqt = (nqg + wq - 1) / wq;
     const int64_t segs_per_wg = static_cast<int64_t>(p.ws) * kLaneSegs;
     p.nst = static_cast<int32_t>((segs + segs_per_wg - 1) / segs_per_wg);
-    const int64_t tiles = nhalf * H * static_cast<int64_t>(p.nqt) * p.nst;
-    if (tiles >= want || waves == 4) {
-      p.partial_last = p.nst > 1 && segs % segs_per_wg != 0;
-      break;
-    }
+    return nhalf * H * static_cast<int64_t>(p.nqt) * p.nst;
+  };
+  int waves = max_waves;
+  int64_t tiles = shape(waves);
+  while (tiles < want && waves > 4) tiles = shape(waves /= 2);
+  // Short of `want` at 4 waves: 2-wave tiles when they lower the most work a
+  // CU gets (tiles per CU rounded up, times waves per tile).  Restore / pack
+  // of Llama-3-8B geometry, us / GB/s: 2048 tokens 6.87 -> 5.61 / 2515 ->
+  // 2793, 6144 tokens 14.1 -> 12.0 / 3650 -> 4644; where it is a tie (4096,
+  // 7168 tokens) 2-wave tiles ran up to 15% slower.  Not for the staged pack
+  // (wq_max 1), whose workgroups hold LDS rounds for 4 waves or more.
+  if (tiles < want && waves == 4 && wq_max != 1) {
+    const int64_t load4 = (tiles + cus - 1) / cus * 4;
+    const int64_t tiles2 = shape(2);
+    if ((tiles2 + cus - 1) / cus * 2 < load4)
+      tiles = tiles2;
+    else
+      tiles = shape(4);
   }
+  const int64_t segs_per_wg = static_cast<int64_t>(p.ws) * kLaneSegs;
+  p.partial_last = p.nst > 1 && segs % segs_per_wg != 0;
 }
 
 // Workgroup shape of a batched restore: set_grid_dims' rule with the launch
