@@ -1704,10 +1704,10 @@ void set_batch_grid(RowsBatch& b, int64_t H, int64_t C) {
     const int64_t segs_per_wg = static_cast<int64_t>(p.ws) * kLaneSegs;
     return (segs + segs_per_wg - 1) / segs_per_wg;
   };
-  for (int waves = kRowsMaxWaves;; waves /= 2) {
+  auto shape = [&](int waves) {
     const int wq_cap = waves == kRowsMaxWaves ? kRowsWq : 2;
     int wq = 1;
-    while (wq < wq_cap && wq * 2 <= nqg) wq *= 2;
+    while (wq < wq_cap && wq * 2 <= nqg && wq * 2 <= waves) wq *= 2;
     p.waves = waves;
     p.wq = wq;
     p.ws = waves / wq;
@@ -1715,7 +1715,18 @@ void set_batch_grid(RowsBatch& b, int64_t H, int64_t C) {
     int64_t tiles = 0;
     for (int r = 0; r < b.nreq; ++r)
       tiles += 2 * H * p.nqt * nst_of(b.req[r].row_tokens - b.req[r].token0);
-    if (tiles >= want || waves == 4) break;
+    return tiles;
+  };
+  int waves = kRowsMaxWaves;
+  int64_t tiles = shape(waves);
+  while (tiles < want && waves > 4) tiles = shape(waves /= 2);
+  // short of `want` at 4 waves: 2-wave tiles when they lower the most work a
+  // CU gets, as set_grid_dims does for one request
+  if (tiles < want && waves == 4) {
+    const int64_t cus = device_cu_count();
+    const int64_t load4 = (tiles + cus - 1) / cus * 4;
+    const int64_t tiles2 = shape(2);
+    if ((tiles2 + cus - 1) / cus * 2 >= load4) shape(4);
   }
   const int64_t per = 2 * H * static_cast<int64_t>(p.nqt);  // tiles per token tile
   const int64_t tile_tokens = static_cast<int64_t>(p.ws) * kLaneSegs * kSegTokens;
