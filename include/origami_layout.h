@@ -74,6 +74,16 @@ const char* origami_last_error(void);
 int origami_abi_version(void);
 
 /*
+ * Totals since the library was loaded: chunk plans created (one per distinct
+ * chunk metadata seen by an allocating entry point) and device allocations
+ * the library made (plan metadata uploads).  Either pointer may be null.
+ * New; no reference counterpart: lets a caller (and the tests) check that a
+ * call such as the allocation-free restore created no plan and allocated
+ * no device memory.
+ */
+void origami_debug_counters(int64_t* plans_created, int64_t* device_allocations);
+
+/*
  * Caps the number of workgroups of the row kernels (the fused restore / save
  * and the fast unpack / pack paths) launched later on the calling thread;
  * each workgroup then loops over several tiles.  0 restores the default (one

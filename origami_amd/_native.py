@@ -65,7 +65,8 @@ _SIGNATURES: dict[str, list] = {
         _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p],
 }
 
-EXPORTED_SYMBOLS = ("origami_last_error", "origami_restore_plan_destroy", *_SIGNATURES)
+EXPORTED_SYMBOLS = ("origami_last_error", "origami_restore_plan_destroy",
+                    "origami_debug_counters", *_SIGNATURES)
 
 _lib: ctypes.CDLL | None = None
 _lock = threading.Lock()
@@ -100,6 +101,8 @@ def lib() -> ctypes.CDLL:
             L.origami_set_rows_grid_limit.restype = ctypes.c_int64
             L.origami_restore_plan_destroy.restype = None
             L.origami_restore_plan_destroy.argtypes = [_p]
+            L.origami_debug_counters.restype = None
+            L.origami_debug_counters.argtypes = [_p, _p]
             if L.origami_abi_version() != ABI_VERSION:
                 raise RuntimeError("liborigami_layout.so ABI version mismatch; rebuild it")
             _lib = L
@@ -135,3 +138,10 @@ def i64_array(values) -> np.ndarray:
 def set_rows_grid_limit(max_workgroups: int) -> int:
     """Caps row-kernel workgroups for launches on this thread; returns the old cap."""
     return int(lib().origami_set_rows_grid_limit(int(max_workgroups)))
+
+
+def debug_counters() -> tuple[int, int]:
+    """(chunk plans created, device allocations made) by the library so far."""
+    plans, allocs = ctypes.c_int64(0), ctypes.c_int64(0)
+    lib().origami_debug_counters(ctypes.byref(plans), ctypes.byref(allocs))
+    return int(plans.value), int(allocs.value)

@@ -46,12 +46,29 @@ def hipcc() -> str:
 
 
 def build_library(verbose: bool = False) -> Path:
+    """Compiles each HIP source to an object (in parallel; no device code is
+    shared between them), then links the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", *map(str, SOURCES), "-o", str(tmp)]
-    if verbose:
+    obj_dir = LIB_DIR / "obj"
+    obj_dir.mkdir(exist_ok=True)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    jobs = []
+    for src in SOURCES:
+        obj = obj_dir / (src.stem + ".o")
+        jobs.append([hipcc(), *compile_flags, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)])
+    for cmd in jobs if verbose else ():
         print(" ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
+    with ThreadPoolExecutor(max_workers=len(jobs)) as pool:
+        for fut in [pool.submit(subprocess.run, cmd, check=True) for cmd in jobs]:
+            fut.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *[j[-1] for j in jobs],
+            "-o", str(tmp)]
+    if verbose:
+        print(" ".join(link), flush=True)
+    subprocess.run(link, check=True)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -274,6 +274,9 @@ std::mutex g_plan_mutex;
 std::unordered_map<uint64_t, std::vector<std::shared_ptr<Plan>>> g_plans;
 size_t g_plan_count = 0;         // plans in the cache
 size_t g_plan_device_count = 0;  // of which hold device memory
+// Totals since the library was loaded (origami_debug_counters).
+std::atomic<int64_t> g_plans_created{0};
+std::atomic<int64_t> g_device_allocations{0};
 constexpr size_t kMaxHostPlans = 4096;
 
 uint64_t hash_words(uint64_t h, const int64_t* w, int64_t n) {
@@ -321,6 +324,7 @@ int plan_device(const std::shared_ptr<const Plan>& cplan) {
     plan->dev = nullptr;
     return fail(ORIGAMI_ERR_HIP, "hipMalloc of the layout plan failed");
   }
+  g_device_allocations.fetch_add(1, std::memory_order_relaxed);
   if (hipMemcpy(plan->dev, plan->host.data(), words * sizeof(int64_t), hipMemcpyHostToDevice) !=
       hipSuccess) {
     (void)hipFree(plan->dev);
@@ -390,6 +394,7 @@ int get_plan(const int64_t* offsets, const int64_t* bits, const int64_t* specs,
   *out = plan;
   g_plans[h].push_back(std::move(plan));
   ++g_plan_count;
+  g_plans_created.fetch_add(1, std::memory_order_relaxed);
   return ORIGAMI_OK;
 }
 
@@ -1541,37 +1546,71 @@ struct BlockCopyParams {
 
 // SCATTER: token-major value -> cache rows (zero rows for t >= T).
 // GATHER:  cache rows -> token-major value.
-template <bool SCATTER, int VEC>
-__global__ __launch_bounds__(kThreads) void block_copy_kernel(BlockCopyParams p) {
-  const int64_t vec_per_row = p.row_bytes / VEC;
+// Byte path (rows not a multiple of 16 bytes, or unaligned buffers): one
+// thread per byte.
+template <bool SCATTER>
+__global__ __launch_bounds__(kThreads) void block_copy_bytes_kernel(BlockCopyParams p) {
   const int64_t rows_per_half = p.block_count * p.bs;
-  const int64_t total = 2 * rows_per_half * vec_per_row;
+  const int64_t total = 2 * rows_per_half * p.row_bytes;
   const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
        idx += step) {
-    const int64_t v = idx % vec_per_row;
-    const int64_t r = idx / vec_per_row;
+    const int64_t v = idx % p.row_bytes;
+    const int64_t r = idx / p.row_bytes;
     const int64_t t = r % rows_per_half;
     const int64_t half = r / rows_per_half;
     const int64_t blk = t / p.bs;
     const int64_t pid = p.block_ids[blk];
     if (pid < 0 || pid >= p.num_blocks) continue;
-    const int64_t cache_row = pid * p.blk_stride + half * p.half_stride + (t - blk * p.bs);
-    const int64_t cache_off = cache_row * p.row_bytes + v * VEC;
-    if constexpr (SCATTER) {
-      if constexpr (VEC == 16) {
-        uint4 x = make_uint4(0, 0, 0, 0);
-        if (t < p.T) x = *reinterpret_cast<const uint4*>(p.src + (half * p.T + t) * p.row_bytes + v * 16);
-        *reinterpret_cast<uint4*>(p.dst + cache_off) = x;
-      } else {
-        p.dst[cache_off] = t < p.T ? p.src[(half * p.T + t) * p.row_bytes + v] : 0;
+    const int64_t cache_off =
+        (pid * p.blk_stride + half * p.half_stride + (t - blk * p.bs)) * p.row_bytes + v;
+    if constexpr (SCATTER)
+      p.dst[cache_off] = t < p.T ? p.src[(half * p.T + t) * p.row_bytes + v] : 0;
+    else
+      p.dst[(half * p.Tt + t) * p.row_bytes + v] = p.src[cache_off];
+  }
+}
+
+// 16-byte path: one workgroup per (half, block) pair.  A block's bs rows are
+// one contiguous run of the cache (both layouts) and of the token-major
+// value, so the workgroup copies bs * row_bytes contiguous bytes, 16 per
+// lane, kBlockCopyUnroll loads in flight per lane before their stores; rows
+// past T are written as zeros.  Each byte is read and written once:
+// non-temporal accesses.
+constexpr int kBlockCopyUnroll = 8;
+
+template <bool SCATTER>
+__global__ __launch_bounds__(kThreads) void block_copy_kernel(BlockCopyParams p) {
+  const int64_t items = 2 * p.block_count;
+  const int64_t run = p.bs * p.row_bytes;  // bytes of one block-half
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    const int64_t half = item / p.block_count;
+    const int64_t blk = item - half * p.block_count;
+    const int64_t pid = p.block_ids[blk];
+    if (pid < 0 || pid >= p.num_blocks) continue;
+    uint8_t* const cache = SCATTER ? p.dst : const_cast<uint8_t*>(p.src);
+    uint8_t* const crun = cache + (pid * p.blk_stride + half * p.half_stride) * p.row_bytes;
+    const int64_t t0 = blk * p.bs;
+    // value bytes of this block-half that hold tokens (scatter: rows below T)
+    const int64_t valid =
+        SCATTER ? (p.T - t0 >= p.bs ? run : p.T > t0 ? (p.T - t0) * p.row_bytes : 0) : run;
+    const uint8_t* const src =
+        SCATTER ? p.src + (half * p.T + t0) * p.row_bytes : crun;
+    uint8_t* const dst = SCATTER ? crun : p.dst + (half * p.Tt + t0) * p.row_bytes;
+    constexpr int64_t kStep = static_cast<int64_t>(kThreads) * 16;
+    for (int64_t base = static_cast<int64_t>(threadIdx.x) * 16; base < run;
+         base += kStep * kBlockCopyUnroll) {
+      u32x4 x[kBlockCopyUnroll];
+#pragma unroll
+      for (int u = 0; u < kBlockCopyUnroll; ++u) {
+        const int64_t off = base + u * kStep;
+        x[u] = u32x4{0u, 0u, 0u, 0u};
+        if (off < valid) x[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + off));
       }
-    } else {
-      const int64_t val_off = (half * p.Tt + t) * p.row_bytes + v * VEC;
-      if constexpr (VEC == 16) {
-        *reinterpret_cast<uint4*>(p.dst + val_off) = *reinterpret_cast<const uint4*>(p.src + cache_off);
-      } else {
-        p.dst[val_off] = p.src[cache_off];
+#pragma unroll
+      for (int u = 0; u < kBlockCopyUnroll; ++u) {
+        const int64_t off = base + u * kStep;
+        if (off < run) __builtin_nontemporal_store(x[u], reinterpret_cast<u32x4*>(dst + off));
       }
     }
   }
@@ -1600,6 +1639,15 @@ void set_stream(RowsParams& p, const uint8_t* flat, int64_t flat_bytes) {
   p.stream = reinterpret_cast<uint8_t*>(base);
   p.bit_bias = static_cast<int64_t>(addr - base) * 8;
   p.stream_bytes = flat_bytes + static_cast<int64_t>(addr - base);
+}
+
+// A kRowsBits pack ORs its runs into the stream, so the chunks' bytes
+// [offsets[0], offsets[n]) are cleared first; bytes of the caller's buffer
+// outside them are left as they are.
+int clear_bits_stream(int mode, uint8_t* flat, const int64_t* offsets, int64_t n,
+                      hipStream_t stream) {
+  if (mode != kRowsBits || n <= 0) return ORIGAMI_OK;
+  return launch_fill_zero(flat + offsets[0], offsets[n] - offsets[0], stream);
 }
 
 // Points the row kernels at the plan's plane offsets: the closed form of a
@@ -2073,12 +2121,8 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
       return fail(ORIGAMI_ERR_INVALID, "staged pack workgroups have 4, 8 or 16 waves");
     return check_launch("rows_pack_staged8_kernel");
   }
-  if (mode == kRowsBits) {
-    if (!pack || bits >= 8) return fail(ORIGAMI_ERR_INVALID, "bit rows mode is a sub-byte pack");
-    // the runs are ORed in: clear the caller's stream bytes first
-    const int64_t lead = p.bit_bias >> 3;
-    if (int rc = launch_fill_zero(p.stream + lead, p.stream_bytes - lead, stream)) return rc;
-  }
+  if (mode == kRowsBits && (!pack || bits >= 8))
+    return fail(ORIGAMI_ERR_INVALID, "bit rows mode is a sub-byte pack");
   const bool window = mode == kRowsWindow;
 #define ORIGAMI_ROWS_CASE(B)                                                          \
   case B:                                                                             \
@@ -2325,6 +2369,8 @@ int fill_plane_table(int64_t* table, const int64_t* offsets, const int64_t* spec
 struct origami_restore_plan {
   std::shared_ptr<const Plan> plan;  // keeps a reordered plan's device table alive
   RowsParams p;                      // stream and rows set per launch
+  RowsParams pw;                     // the same with the wide-run grid (b = 1, 2, 4)
+  bool has_wide = false;
   int64_t stream_bytes = 0;          // chunk_offsets[num_chunks]
   int64_t tokens = 0;
   int device = 0;
@@ -2335,6 +2381,12 @@ extern "C" {
 const char* origami_last_error(void) { return g_last_error.c_str(); }
 
 int origami_abi_version(void) { return 3; }
+
+void origami_debug_counters(int64_t* plans_created, int64_t* device_allocations) {
+  if (plans_created) *plans_created = g_plans_created.load(std::memory_order_relaxed);
+  if (device_allocations)
+    *device_allocations = g_device_allocations.load(std::memory_order_relaxed);
+}
 
 int64_t origami_set_rows_grid_limit(int64_t max_workgroups) {
   const int64_t previous = g_rows_grid_limit;
@@ -2466,6 +2518,8 @@ int origami_pack_canonical_storage_chunks(
     p.bs = T;
     const int mode = pack_mode(plan->info, p, T);
     set_pack_grid(p, mode, H, C, T, 1);
+    if (int rc2 = clear_bits_stream(mode, flat_chunks, chunk_offsets, num_chunks, stream))
+      return rc2;
     return launch_rows(true, p, 1, plan->info.bits, mode, stream);
   }
 
@@ -2540,6 +2594,14 @@ int origami_restore_plan_create(const int64_t* chunk_offsets, const int64_t* bit
   rp->p = fused_restore_params(nullptr, 0, tokens, nullptr, num_blocks, block_size, num_heads,
                                head_bytes, block_ids, block_count, blk_stride, half_stride);
   if (int rc2 = set_planes(rp->p, plan)) return rc2;
+  const int bits = plan->info.bits;
+  if (bits == 1 || bits == 2 || bits == 4) {
+    // the wide 16-byte-run restore applies when the stream pointer passed to
+    // a launch is aligned (rows_mode decides per launch)
+    rp->pw = rp->p;
+    set_restore_grid(rp->pw, kRowsWide, bits, num_heads, head_bytes, rp->p.row_tokens, 2);
+    rp->has_wide = true;
+  }
   set_grid_dims(rp->p, num_heads, head_bytes, rp->p.row_tokens, 2);
   *out = rp.release();
   return ORIGAMI_OK;
@@ -2558,9 +2620,13 @@ int origami_restore_plan_launch(origami_restore_plan_t plan, const uint8_t* flat
     return fail(ORIGAMI_ERR_INVALID, "restore plan launched on another device than it was made on");
   RowsParams p = plan->p;
   set_stream(p, flat_chunks, flat_bytes);
+  const int mode = rows_mode(plan->plan->info, p, plan->tokens, false, 0, plan->has_wide);
+  if (mode == kRowsWide || mode == kRowsWideCached) {
+    p = plan->pw;
+    set_stream(p, flat_chunks, flat_bytes);
+  }
   p.rows = static_cast<uint8_t*>(kv_cache);
-  return launch_rows(false, p, 2, plan->plan->info.bits,
-                     rows_mode(plan->plan->info, p, plan->tokens, false),
+  return launch_rows(false, p, 2, plan->plan->info.bits, mode,
                      reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -2602,8 +2668,9 @@ int origami_unpack_canonical_to_kv_cache_noalloc(
       return rc2;
     p.planes = table;
   }
-  set_grid_dims(p, num_heads, head_bytes, p.row_tokens, 2);
-  return launch_rows(false, p, 2, info.bits, rows_mode(info, p, tokens, false), stream);
+  const int mode = rows_mode(info, p, tokens, false, 0, true);
+  set_restore_grid(p, mode, info.bits, num_heads, head_bytes, p.row_tokens, 2);
+  return launch_rows(false, p, 2, info.bits, mode, stream);
 }
 
 int origami_unpack_canonical_to_kv_cache_batch(
@@ -2728,6 +2795,8 @@ int origami_pack_canonical_from_kv_cache(
   p.half_stride = half_stride;
   const int mode = pack_mode(plan->info, p, tokens);
   set_pack_grid(p, mode, num_heads, head_bytes, tokens, 2);
+  if (int rc2 = clear_bits_stream(mode, flat_chunks, chunk_offsets, num_chunks, stream))
+    return rc2;
   return launch_rows(true, p, 2, plan->info.bits, mode, stream);
 }
 
@@ -2755,20 +2824,21 @@ static int block_copy(bool scatter, const uint8_t* src, uint8_t* dst, int64_t to
   int rc = cache_geometry(cache_layout, num_blocks, block_size, &p.blk_stride, &p.half_stride);
   if (rc) return rc;
   const bool vec = p.row_bytes % 16 == 0 && aligned16(src) && aligned16(dst);
-  const int64_t work = 2 * p.Tt * (vec ? p.row_bytes / 16 : p.row_bytes);
-  const dim3 grid(grid_for(work, kThreads, 65536)), block(kThreads);
-  if (scatter) {
-    if (vec)
-      hipLaunchKernelGGL((block_copy_kernel<true, 16>), grid, block, 0, stream, p);
+  const dim3 block(kThreads);
+  if (vec) {
+    const dim3 grid(static_cast<unsigned>(std::min<int64_t>(2 * block_count, 1 << 20)));
+    if (scatter)
+      hipLaunchKernelGGL(block_copy_kernel<true>, grid, block, 0, stream, p);
     else
-      hipLaunchKernelGGL((block_copy_kernel<true, 1>), grid, block, 0, stream, p);
-  } else {
-    if (vec)
-      hipLaunchKernelGGL((block_copy_kernel<false, 16>), grid, block, 0, stream, p);
-    else
-      hipLaunchKernelGGL((block_copy_kernel<false, 1>), grid, block, 0, stream, p);
+      hipLaunchKernelGGL(block_copy_kernel<false>, grid, block, 0, stream, p);
+    return check_launch("block_copy_kernel");
   }
-  return check_launch("block_copy_kernel");
+  const dim3 grid(grid_for(2 * p.Tt * p.row_bytes, kThreads, 65536));
+  if (scatter)
+    hipLaunchKernelGGL(block_copy_bytes_kernel<true>, grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL(block_copy_bytes_kernel<false>, grid, block, 0, stream, p);
+  return check_launch("block_copy_bytes_kernel");
 }
 
 int origami_scatter_kv_blocks(const uint8_t* value, int64_t tokens, void* kv_cache,

@@ -71,6 +71,30 @@ def test_fused_save_runs_at_any_bit(cuda_device, T, bits, shift):
         "bytes outside the stream were written"
 
 
+@pytest.mark.parametrize("T,bits,shift", [(4099, 7, 1), (2053, 3, 0)])
+def test_fused_save_into_larger_output(cuda_device, T, bits, shift):
+    """An output buffer longer than the stream: the pack writes the stream's
+    bytes only, and the buffer's tail past them keeps its guard value."""
+    dev = cuda_device
+    rng = np.random.default_rng(T * 7 + bits)
+    nblk = -(-T // BS)
+    NB = nblk + 3
+    cache_u8 = rng.integers(0, 1 << bits, (2, NB, BS, H, C), dtype=np.uint8)
+    cache = torch.from_numpy(cache_u8).to(dev).view(torch.bfloat16)
+    table = rng.permutation(NB)[:nblk].astype(np.int64)
+    specs = _specs(2 * T)
+    lay = kv_symbol_layout(T, H, C, bits, specs)
+    buf = torch.full((lay.stream_bytes + shift + 4099,), 0x5A, dtype=torch.uint8, device=dev)
+    native_gpu.pack_from_kv_cache(cache, native_gpu.block_ids_tensor(table, dev, NB), T, lay,
+                                  buf[shift:])
+    sym = oracle.gather_kv_cache(cache_u8, table).reshape(2, -1, H, C)[:, :T].reshape(-1)
+    flat, _ = oracle.pack_canonical(sym, bits, specs, [2 * T, H, C], [0, 1, 2, -1])
+    host = buf.cpu().numpy()
+    assert np.array_equal(host[shift:shift + lay.stream_bytes], flat), "pack differs from the oracle"
+    assert (host[:shift] == 0x5A).all() and (host[shift + lay.stream_bytes:] == 0x5A).all(), \
+        "bytes outside the stream were written"
+
+
 @pytest.mark.parametrize("T,bits,target", [(2051, 3, 1 << 15), (1027, 7, 1 << 14), (4096, 5, 3000)])
 def test_storage_pack_runs_at_any_bit(cuda_device, T, bits, target):
     """A [T, H, C] symbol tensor packed with small chunks (planes split

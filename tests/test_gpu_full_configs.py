@@ -7,7 +7,8 @@
 * Llama-3-8B fp8 e4m3: 8 KV heads, head_dim 128 (128-byte head rows), 16
   requests of 16384 tokens, seed 3;
 * Llama-3-70B geometry: one 131072-token bf16 layer, 512 chunks of 1 MiB,
-  permuted block table, seed 4 (stream bit offsets pass 2**32).
+  permuted block table, seed 4 (stream bit offsets pass 2**32);
+* one TP = 8 rank's share of the 32768-token Llama-3-8B layer: 1 KV head.
 
 Chunks come from the planner at 1 MiB (chunking.py:22-123).  For every
 request the HIP pack from the paged cache must equal the oracle's pack of
@@ -127,6 +128,16 @@ def test_llama3_8b_fp8_16x16k_full(cuda_device):
 
 def test_llama3_70b_131072_full(cuda_device):
     _run(cuda_device, 8, 128, torch.bfloat16, [131072], 4, False, expect_chunks=512)
+
+
+@pytest.mark.parametrize("T", [32768, 32753])
+def test_llama3_8b_tp8_rank_share_full(cuda_device, T):
+    """One tensor-parallel rank's share of the 32768-token Llama-3-8B layer
+    at TP = 8 (config.py:312-320 gives each rank its own KV heads): 1 KV
+    head, head_dim 128, bf16 (256-byte rows), 16 chunks of 1 MiB, permuted
+    block table; and the same at a ragged length."""
+    _run(cuda_device, 1, 128, torch.bfloat16, [T], 8, False,
+         expect_chunks=16 if T == 32768 else None)
 
 
 def test_batch_split_launch_block_size_24(cuda_device):

@@ -338,10 +338,15 @@ def test_irregular_plan_restore_falls_back_and_matches(cuda_device):
     assert np.array_equal(cache_gpu.cpu().numpy(), expect)
 
 
+@pytest.mark.parametrize("tokens,H,C,bs", [
+    (1234, 8, 256, 16),   # 32 KiB block-halves, partial last block
+    (1000, 4, 512, 40),   # 80 KiB block-halves: three unrolled rounds per workgroup
+    (77, 2, 48, 24),      # 96-byte rows
+    (300, 3, 20, 8),      # 60-byte rows: the byte path
+])
 @pytest.mark.parametrize("blocks_first", [False, True])
-def test_block_scatter_and_gather_match_oracle(cuda_device, blocks_first):
-    rng = np.random.default_rng(11)
-    tokens, H, C, bs = 1234, 8, 256, 16
+def test_block_scatter_and_gather_match_oracle(cuda_device, blocks_first, tokens, H, C, bs):
+    rng = np.random.default_rng(11 + tokens)
     value = rng.integers(0, 256, (2, tokens, H, C), dtype=np.uint8)
     ids, cache = _kv_case(rng, tokens, H, C, bs, blocks_first)
     expect = cache.copy()

@@ -44,6 +44,10 @@ def _specs(kind, T, H, C, rng, target=1 << 14):
     ("reordered", 1000, 8, 16, False),
     ("reordered_partial", 777, 3, 8, True),
     ("planner", 4096, 5, 16, False),
+    # b = 1, 2, 4 with T a multiple of 128 / b: the wide 16-byte-run restore
+    ("planner", 2048, 1, 16, True),
+    ("planner", 2048, 2, 24, False),
+    ("reordered", 1024, 4, 8, False),
 ])
 def test_prepared_restore_matches_fused_and_oracle(cuda_device, kind, T, bits, bs,
                                                    blocks_first):

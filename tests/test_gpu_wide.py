@@ -77,6 +77,21 @@ def test_wide_runs_off_lines(cuda_device, bits):
     _restore_case(cuda_device, 4096 + 128 // bits, 8, 256, bits, bs=32, seed=10 + bits)
 
 
+@pytest.mark.parametrize("bits,T,bs,blocks_first", [
+    (4, 4096, 8, False),              # on lines, a lane's 16-row sub-tiles span two blocks
+    (2, 4096, 24, True),              # on lines, sub-tiles cross 24-row block boundaries
+    (1, 4096, 24, False),
+    (4, 4096 + 32, 24, False),        # off lines (cached runs), partial last block
+    (2, 4096 + 64, 8, True),
+    (1, 4096 + 128, 8, False),
+])
+def test_wide_runs_block_sizes_off_16(cuda_device, bits, T, bs, blocks_first):
+    # block sizes that are not a multiple of 16: the row stores follow the
+    # block table row by row
+    _restore_case(cuda_device, T, 8, 256, bits, bs=bs, blocks_first=blocks_first,
+                  seed=70 + bits + bs)
+
+
 @pytest.mark.parametrize("bits,T", [(4, 4096 + 16), (2, 4096 + 32), (1, 4096 + 64)])
 def test_token_count_off_the_run_falls_back(cuda_device, bits, T):
     _restore_case(cuda_device, T, 8, 256, bits, seed=20 + bits)

@@ -3,8 +3,10 @@ called through the C ABI, gives byte for byte what
 origami_unpack_canonical_to_kv_cache gives, on two calls in a row (the
 second with a smaller layer), for chunk plans in the planner's order (no
 device metadata) and reordered ones (plane table in the fixed scratch
-array, rewritten by every call), and rejects a reordered plan above the
-scratch maximum."""
+array, rewritten by every call), at b = 8, 5 and in the wide 16-byte-run
+mode (b = 4, 2); it creates no plan and makes no device allocation; it can
+be captured in a HIP graph whose replays restore new stream contents; and
+it rejects a reordered plan above the scratch maximum."""
 import numpy as np
 import pytest
 import torch
@@ -103,3 +105,86 @@ def test_noalloc_rejects_reordered_plan_above_scratch_maximum(cuda_device):
     # the allocating entry point serves it (its plane table is allocated)
     _restore(FUSED, flat, lay, T, cache, ids)
     torch.cuda.synchronize(cuda_device)
+
+
+@pytest.mark.parametrize("kind", ["planner", "reordered"])
+def test_noalloc_wide_runs_twice(cuda_device, kind):
+    """b = 4 then b = 2 (token counts multiples of 128 / b): the wide
+    16-byte-run restore, second call smaller."""
+    rng = np.random.default_rng(300)
+    _case(cuda_device, rng, kind, 1024, 8, 256, 4, 16, False)
+    _case(cuda_device, rng, kind, 512, 4, 128, 2, 16, True)
+
+
+def test_noalloc_creates_no_plan_and_allocates_nothing(cuda_device):
+    dev = cuda_device
+    rng = np.random.default_rng(11)
+    calls = []
+    for kind, T, bits in (("planner", 700, 8), ("reordered", 700, 8),
+                          ("reordered_partial", 512, 4), ("planner", 1024, 2)):
+        H, C, bs = 4, 128, 16
+        nblk = -(-T // bs)
+        NB = nblk + 3
+        specs = _specs(kind, T, H, C, rng)
+        lay = kv_symbol_layout(T, H, C, bits, specs)
+        flat = torch.from_numpy(rng.integers(0, 256, lay.stream_bytes, dtype=np.uint8)).to(dev)
+        cache = torch.zeros((2, NB, bs, H, C), dtype=torch.uint8, device=dev)
+        ids = torch.from_numpy(rng.permutation(NB)[:nblk].astype(np.int64)).to(dev)
+        calls.append((flat, lay, T, cache, ids))
+    before = _native.debug_counters()
+    for _ in range(2):
+        for c in calls:
+            _restore(NOALLOC, *c)
+    torch.cuda.synchronize(dev)
+    assert _native.debug_counters() == before
+    # the allocating entry point, on the same reordered plan, creates a plan
+    # and uploads its plane table (the counters see both)
+    _restore(FUSED, *calls[1])
+    torch.cuda.synchronize(dev)
+    after = _native.debug_counters()
+    assert after[0] > before[0] and after[1] > before[1]
+
+
+@pytest.mark.parametrize("kind,bits", [("planner", 8), ("reordered", 8), ("reordered", 3)])
+def test_noalloc_graph_capture_replays(cuda_device, kind, bits):
+    """The restore captured once (single stream, kernels only); each replay
+    after new stream bytes are copied into the captured input restores
+    them, checked against the allocating entry point and the oracle, with
+    eager work and synchronisation between the replays."""
+    dev = cuda_device
+    rng = np.random.default_rng(400 + bits)
+    T, H, C, bs = 1000, 8, 256, 16
+    nblk = -(-T // bs)
+    NB = nblk + 5
+    specs = _specs(kind, T, H, C, rng)
+    lay = kv_symbol_layout(T, H, C, bits, specs)
+    ids_np = rng.permutation(NB)[:nblk].astype(np.int64)
+    ids = torch.from_numpy(ids_np).to(dev)
+    flat = torch.zeros(lay.stream_bytes, dtype=torch.uint8, device=dev)
+    cache = torch.zeros((2, NB, bs, H, C), dtype=torch.uint8, device=dev)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        _restore(NOALLOC, flat, lay, T, cache, ids)  # warm-up outside the capture
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _restore(NOALLOC, flat, lay, T, cache, ids)
+    for replay in range(3):
+        sym = rng.integers(0, 256, 2 * T * H * C, dtype=np.uint8)
+        flat_np, offs = oracle.pack_canonical(sym, bits, specs, [2 * T, H, C], [0, 1, 2, -1])
+        flat.copy_(torch.from_numpy(flat_np).to(dev))
+        cache.fill_(0x5A)
+        torch.cuda.synchronize(dev)
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        ref = torch.full_like(cache, 0x5A)
+        _restore(FUSED, flat, lay, T, ref, ids)
+        torch.cuda.synchronize(dev)
+        got = cache.cpu().numpy()
+        assert np.array_equal(got, ref.cpu().numpy()), (kind, bits, replay)
+        expect = np.full(cache.shape, 0x5A, dtype=np.uint8)
+        oracle.restore_layer(flat_np, offs, bits, specs, T, H, C, ids_np, expect)
+        assert np.array_equal(got, expect), (kind, bits, replay)
+    del graph
