@@ -298,6 +298,12 @@ def main() -> int:
 
     if not args.no_connector:
         result["connector"] = connector_leg(dev, args.connector_layers, T, H, D, bs)
+        cb = connector_batch_leg(dev)
+        qwen = result.get("configs", {}).get("qwen2.5-7b-batch")
+        if qwen:
+            cb["kernel_vs_configs_batched"] = round(
+                cb["batched"]["kernel_us_per_layer"] / qwen["per_layer_us"], 4)
+        result["connector_batch"] = cb
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(streams[0], layout, specs, T, H, C, bs, NB,
@@ -888,6 +894,125 @@ def connector_leg(dev, layers, T, H, D, bs):
     }
 
 
+def connector_batch_leg(dev, layers=4):
+    """The Qwen2.5-7B batch (4 KV heads, head_dim 128, bf16, bs 16; 8
+    requests of default_rng(2).integers(8192, 65537, 8) tokens saved as whole
+    blocks, each table's first half from a shared prefix pool) restored
+    through the connector's drop-in surface: one start_load_kv for the 8
+    requests, wait_for_layer_load for each of `layers` layers.  The CPU codec
+    is "raw" (a copy), so decompression does not hide the device work.  The
+    kernel time per layer is what the worker's own event-timed metric rows
+    (bitunpack_cuda) record for the restore launches of the layer, summed
+    over its launches; `batched` restores each layer of the batch with one
+    H2D and one launch, `per_request` with origami_batch_restores off (one
+    launch per request and layer, as the reference's per-request threads).
+    Each restored cache is checked against the saved source blocks."""
+    import json as _json
+    import tempfile
+    import types
+
+    import numpy as np
+    import torch
+
+    from origami_amd.connector import KVConnectorRole, OrigamiConnector
+    from origami_amd.metadata import (OrigamiConnectorMetadata, OrigamiRestoreRequest,
+                                      OrigamiSaveRequest)
+    from origami_amd.synthetic import fill_layer
+
+    H, D, bs = 4, 128, 16
+    lengths = [int(T) for T in np.random.default_rng(2).integers(8192, 65537, 8)]
+    nblks = [-(-T // bs) for T in lengths]
+    shared = [T // 2 // bs for T in lengths]
+    pool = max(shared)
+    NB = pool + sum(n - k for n, k in zip(nblks, shared)) + 64
+    rng = np.random.default_rng(2)
+
+    def tables():
+        perm = rng.permutation(NB)
+        cur, ts = pool, []
+        for n, k in zip(nblks, shared):
+            ts.append([int(b) for b in np.concatenate([perm[:k], perm[cur:cur + n - k]])])
+            cur += n - k
+        return ts
+
+    names = [f"model.layers.{i}.self_attn.attn" for i in range(layers)]
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    src = {}
+    for n in names:
+        src[n] = torch.zeros((2, NB, bs, H, D), dtype=torch.bfloat16, device=dev)
+        fill_layer(src[n], torch.arange(NB, device=dev), gen)
+    src_t, dst_t = tables(), tables()
+    mdir = tempfile.mkdtemp(prefix="origami-bench-")
+
+    def connector(ns, batch, metrics=""):
+        cfg = types.SimpleNamespace(kv_transfer_config=types.SimpleNamespace(
+            kv_connector_extra_config={
+                "origami_quantizer": "raw_byte_planes", "origami_lossless_cpu_backend": "raw",
+                "origami_store_uri": f"memory://{ns}", "origami_qat_threads": 16,
+                "origami_metrics_dir": metrics, "origami_batch_restores": batch}))
+        return OrigamiConnector(cfg, KVConnectorRole.WORKER)
+
+    saver = connector("bench-batch", True)
+    saver.register_kv_caches(src)
+    saver.bind_connector_metadata(OrigamiConnectorMetadata(reqs_to_save={
+        f"s{i}": OrigamiSaveRequest(request_id=f"s{i}", cache_key=f"q{i}",
+                                    block_ids_per_group=(tuple(t),), num_tokens=len(t) * bs)
+        for i, t in enumerate(src_t)}))
+    saver.start_load_kv(None)
+    for n in names:
+        saver.save_kv_layer(n, src[n], None)
+    saver.wait_for_save()
+    del saver
+
+    out = {"layers": layers, "requests": len(lengths), "tokens": sum(lengths),
+           "codec": "raw (copy)", "kv_heads": H, "head_dim": D}
+    dst = {n: torch.zeros_like(src[n]) for n in names}
+    reqs = {f"r{i}": OrigamiRestoreRequest(request_id=f"r{i}", cache_key=f"q{i}",
+                                           block_ids_per_group=(tuple(t),),
+                                           num_tokens=len(t) * bs)
+            for i, t in enumerate(dst_t)}
+    for label, batch in (("batched", True), ("per_request", False)):
+        metrics = f"{mdir}/{label}"
+        loader = connector("bench-batch", batch, metrics)
+        loader.register_kv_caches(dst)
+        worker = loader.connector_worker
+        seen, res = 0, {}
+        # the first pass builds the pipeline and its pinned staging; the
+        # second is reported
+        for _ in range(2):
+            for n in names:
+                dst[n].zero_()
+            loader.bind_connector_metadata(OrigamiConnectorMetadata(reqs_to_restore=reqs))
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            loader.start_load_kv(None)
+            for n in names:
+                loader.wait_for_layer_load(n)
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+            worker.flush_metrics()
+            lines = open(f"{metrics}/origami_metrics.jsonl").read().splitlines()
+            rows = [_json.loads(x) for x in lines[seen:]]
+            seen = len(lines)
+            per_layer = {}
+            for r in rows:
+                if r.get("type") == "bitunpack_cuda":
+                    per_layer[r["layer_name"]] = per_layer.get(r["layer_name"], 0.0) + r["ms"]
+            ok = all(torch.equal(dst[n][:, d].view(torch.int16), src[n][:, s_].view(torch.int16))
+                     for n in names for s_, d in zip(src_t, dst_t))
+            res = {"kernel_us_per_layer": round(1e3 * float(np.median(list(per_layer.values()))),
+                                                 2),
+                   "restore_wall_ms": round(wall * 1e3, 2), "restore_ok": bool(ok),
+                   "launches_per_layer": sum(1 for r in rows if r.get("type") == "bitunpack_cuda")
+                   // max(1, len(per_layer))}
+        worker.shutdown()
+        out[label] = res
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def pipeline_leg(host, layout, T, dst_caches, dst_ids, dev, kernel_ms, layers=None):
     """Layer-wise restore from pinned host memory with the copy of layer L+1
     overlapped with the unpack+scatter of layer L, against the H2D copies
@@ -909,33 +1034,34 @@ def pipeline_leg(host, layout, T, dst_caches, dst_ids, dev, kernel_ms, layers=No
                                   dst_ids[last])
     for c in dst_caches:
         c.zero_()
-    pipe = LayerRestorePipeline(dev, nbytes, num_slots=3, host_staging=False)
+    pipe = LayerRestorePipeline(dev, nbytes, num_lanes=2, host_staging=False)
+    cur = torch.cuda.current_stream(dev)
     torch.cuda.synchronize()
 
-    def copies_only():
+    def run(submit_layer):
         start = torch.cuda.Event(enable_timing=True)
-        start.record(pipe.copy_stream)
-        for layer in range(L):
-            pipe.copy_only(host[layer % len(host)], nbytes)
         end = torch.cuda.Event(enable_timing=True)
-        end.record(pipe.copy_stream)
-        pipe.synchronize()
+        start.record(cur)
+        pipe.begin(cur)
+        for layer in range(L):
+            submit_layer(layer)
+        pipe.join(cur)
+        end.record(cur)
+        torch.cuda.synchronize()
         return start.elapsed_time(end)
 
+    def copies_only():
+        return run(lambda layer: pipe.copy_only(host[layer % len(host)], nbytes))
+
     def pipelined(compute=True):
-        start = torch.cuda.Event(enable_timing=True)
-        start.record(pipe.copy_stream)
-        for layer in range(L):
+        def one(layer):
             h = host[layer % len(host)]
             if compute:
                 k = layer % len(dst_caches)
                 pipe.restore_pinned(h, layout, T, dst_caches[k], dst_ids[k])
             else:
                 pipe.submit(h, nbytes, lambda flat: None)
-        end = torch.cuda.Event(enable_timing=True)
-        end.record(pipe.compute_stream)
-        pipe.synchronize()
-        return start.elapsed_time(end)
+        return run(one)
 
     reps = 3
     copies_only()
@@ -950,23 +1076,21 @@ def pipeline_leg(host, layout, T, dst_caches, dst_ids, dev, kernel_ms, layers=No
         "h2d_ms": round(h2d, 3),
         "h2d_gbps": round(L * nbytes / (h2d * 1e-3) / 1e9, 2),
         "pipelined_restore_ms": round(full, 3),
-        # the same two-stream pipeline with no restore compute: its cost over
-        # the bare copies is the per-layer stream/event handoff
+        # the same lanes with no restore: the lanes' copies overlap each
+        # other, so this can come in under h2d_ms
         "pipelined_no_compute_ms": round(handoff, 3),
+        # what the restore adds over the bare copies
         "exposed_ms": round(full - h2d, 3),
-        "exposed_restore_ms": round(full - handoff, 3),
         "restore_compute_ms": round(L * kernel_ms, 3),
-        # the share of the restore kernels' time that the copies hide
-        "restore_hidden_fraction": round(max(0.0, 1.0 - (full - handoff) / (L * kernel_ms)), 4),
-        # hidden: the restore adds at most two unpacks (the trailing one plus
-        # one of slack) over the identical pipeline without compute
-        "restore_hidden": bool(full - handoff <= 2 * kernel_ms),
-        # the same bound against the bare copies (the pipeline's own stream
-        # and event handoff counted as exposed)
-        "hidden_behind_h2d": bool(full - h2d <= 2 * kernel_ms),
+        # the share of the restore kernels' time the copies hide
+        "restore_hidden_fraction": round(max(0.0, 1.0 - max(0.0, full - h2d) / (L * kernel_ms)),
+                                         4),
+        # hidden: the whole pipeline takes at most the bare copies plus two
+        # unpacks (the trailing one and one of slack)
+        "restore_hidden": bool(full - h2d <= 2 * kernel_ms),
         "restore_ok": ok,
-        "source": (f"pinned host memory ({len(host)} buffers of {nbytes} B), 3 device slots, "
-                   "copy and compute streams"),
+        "source": (f"pinned host memory ({len(host)} buffers of {nbytes} B), 2 lanes (a stream "
+                   "and a device slot each: H2D then restore)"),
     }
 
 

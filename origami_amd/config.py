@@ -32,7 +32,12 @@ class OrigamiConfig:
     dequant_device: str = "auto"
     bitunpack_device: str = "auto"
     fused_attention: str = "off"
-    restore_slots: int = 3
+    # lanes of the layer-wise restore pipeline (one device slot and one stream
+    # each); no reference counterpart
+    restore_slots: int = 2
+    # New (no reference counterpart): the requests of one start_load_kv are
+    # restored together, one H2D copy and one batched launch per layer
+    batch_restores: bool = True
     read_bandwidth_gbps: float = 0.0
     artifact_ingress_mode: str = "file"
     extra: dict[str, Any] = field(default_factory=dict)
@@ -61,7 +66,8 @@ class OrigamiConfig:
             dequant_device=str(get("origami_dequant_device", "auto")).lower(),
             bitunpack_device=str(get("origami_bitunpack_device", "auto")).lower(),
             fused_attention=str(get("origami_fused_attention", "off")).lower(),
-            restore_slots=int(get("origami_restore_slots", 3)),
+            restore_slots=int(get("origami_restore_slots", 2)),
+            batch_restores=bool(get("origami_batch_restores", True)),
             read_bandwidth_gbps=float(get("origami_read_bandwidth_gbps",
                                           get("reuse_read_bandwidth_gbps", 0.0))),
             artifact_ingress_mode=str(get("origami_artifact_ingress_mode",

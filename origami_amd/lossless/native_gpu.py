@@ -381,6 +381,12 @@ class KVRestoreBatch:
         self._specs = [lay.torch_meta[2] for lay in self.layouts]
         self._first_list = [int(x) for x in self._first]
 
+    def record_stream(self, stream: torch.cuda.Stream) -> None:
+        """Marks the device block tables as used on `stream` (restores queued
+        there keep them alive after this object is dropped)."""
+        if self.layouts:
+            self._dev_tables.record_stream(stream)
+
     def restore(self, flats: Sequence[torch.Tensor], kv_cache: torch.Tensor) -> None:
         """Restores one layer: flats[r] is request r's stream on the device."""
         if len(flats) != len(self.layouts):

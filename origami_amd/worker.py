@@ -33,6 +33,7 @@ from pathlib import Path
 from threading import Lock
 from typing import Any
 
+import numpy as np
 import torch
 
 from origami_amd.benchmark_utils import copy_kv_to_hbm, nvtx_range, write_jsonl
@@ -150,7 +151,7 @@ class OrigamiConnectorWorker:
 
     def _make_pipeline(self, index: int, slot_bytes: int) -> LayerRestorePipeline:
         return LayerRestorePipeline(torch.device("cuda", index), slot_bytes,
-                                    num_slots=self.config.restore_slots)
+                                    num_lanes=self.config.restore_slots)
 
     def _lease_pipeline(self, device: torch.device, slot_bytes: int):
         """Context manager holding the device's pipeline (slots of at least
@@ -169,6 +170,7 @@ class OrigamiConnectorWorker:
             "type": "restore_batch_meta", "system": "origami", "restore_count": len(restores),
             "request_ids": [r.request_id for r in restores],
             "cache_keys": [r.cache_key for r in restores], "ts": time.time()})
+        per_request: dict[str, dict[str, Future]] = {}
         for restore in restores:
             layer_futures: dict[str, Future] = {}
             for layer_name in self.kv_caches:
@@ -176,8 +178,21 @@ class OrigamiConnectorWorker:
                 layer_futures[layer_name] = fut
                 self._pending_layer_futures.setdefault(layer_name, []).append(fut)
             self._pending_request_layer_futures[restore.request_id] = list(layer_futures.values())
+            per_request[restore.request_id] = layer_futures
+        if self.config.batch_restores and len(restores) > 1:
+            # one task restores the whole batch; each request still has its
+            # own layer futures and its own completion future
+            done: dict[str, Future] = {}
+            for restore in restores:
+                rf: Future = Future()
+                done[restore.request_id] = rf
+                self._restore_futures.append(rf)
+                self._restore_future_to_request_id[rf] = restore.request_id
+            self._executor.submit(self._restore_batch_layer_futures, restores, per_request, done)
+            return
+        for restore in restores:
             rf = self._executor.submit(self._restore_request_layer_futures, restore,
-                                       layer_futures)
+                                       per_request[restore.request_id])
             self._restore_futures.append(rf)
             self._restore_future_to_request_id[rf] = restore.request_id
 
@@ -204,6 +219,190 @@ class OrigamiConnectorWorker:
                 if not fut.done():
                     fut.set_exception(exc)
             raise
+
+    @staticmethod
+    def _fail_request(layer_futures: dict[str, Future], done: Future, exc: BaseException) -> None:
+        for fut in layer_futures.values():
+            if not fut.done():
+                fut.set_exception(exc)
+        if not done.done():
+            done.set_exception(exc)
+
+    def _restore_batch_layer_futures(self, restores: list[OrigamiRestoreRequest],
+                                     layer_futures: dict[str, dict[str, Future]],
+                                     done: dict[str, Future]) -> None:
+        """The requests of one start_load_kv restored together, layer by layer
+        in model order.  The reference runs one thread per request, each
+        restoring its layers one by one (worker.py:426-481, 796-897); here a
+        layer whose payloads are byte-plane streams is one H2D copy and one
+        batched launch for all requests (_restore_layer_batched), and any
+        other layer goes request by request through _restore_layer.  Each
+        (request, layer) future receives its own outcome; a request whose
+        payload cannot be prepared fails alone."""
+        prepared: dict = {}
+        batches: dict = {}
+        try:
+            payloads: dict[str, OrigamiPayload] = {}
+            for restore in restores:
+                rid = restore.request_id
+                try:
+                    payloads[rid] = self.store.prepare_for_restore(
+                        restore.cache_key, read_bandwidth_gbps=self.config.read_bandwidth_gbps,
+                        metrics_path=self.metrics_path, request_id=rid, system="origami")
+                except Exception as exc:  # noqa: BLE001 - delivered through the futures
+                    self._fail_request(layer_futures[rid], done[rid], exc)
+            live = [r for r in restores if r.request_id in payloads]
+            start_perf = time.perf_counter()
+            for layer_name in self.kv_caches:
+                entries = [(r, layer_futures[r.request_id][layer_name]) for r in live]
+                entries = [(r, f) for r, f in entries if not f.done()]
+                if not entries:
+                    continue
+                try:
+                    rest = self._restore_layer_batched(entries, payloads, layer_name,
+                                                       start_perf, batches)
+                except Exception as exc:  # noqa: BLE001 - delivered through the futures
+                    for _, fut in entries:
+                        if not fut.done():
+                            fut.set_exception(exc)
+                    continue
+                for restore, fut in rest:
+                    try:
+                        result = self._restore_layer(restore, payloads[restore.request_id],
+                                                     layer_name, start_perf, prepared)
+                    except Exception as exc:  # noqa: BLE001
+                        fut.set_exception(exc)
+                    else:
+                        fut.set_result(result)
+            for restore in live:
+                if not done[restore.request_id].done():
+                    done[restore.request_id].set_result(restore.request_id)
+        except Exception as exc:  # noqa: BLE001
+            for restore in restores:
+                self._fail_request(layer_futures[restore.request_id], done[restore.request_id],
+                                   exc)
+        finally:
+            for prep in prepared.values():
+                prep.close()
+
+    def _restore_layer_batched(self, entries, payloads, layer_name: str, start_perf: float,
+                               batches: dict) -> list:
+        """One layer of several requests whose payloads are raw_byte_planes
+        streams ([2T, H, D*e] token-major v2 layouts): every request's chunks
+        are decompressed into one pinned staging buffer (each stream at a
+        256-byte aligned offset), copied to the device in one H2D, and
+        restored by one KVRestoreBatch launch (full blocks that several
+        requests share are read and written once).  Resolves the futures it
+        takes; returns the entries it leaves to the per-request path (other
+        formats, a CPU cache, metadata the per-request path rejects, fewer
+        than two restorable requests)."""
+        kv_cache = self.kv_caches.get(layer_name)
+        if kv_cache is None or not kv_cache.is_cuda:
+            return entries
+        group = self.layer_to_cache_group.get(layer_name, 0)
+        _, nb, bs, H, head_bytes = native_gpu.cache_geometry(kv_cache)
+        items, rest = [], []
+        for restore, fut in entries:
+            lp = payloads[restore.request_id].layer_payloads.get(layer_name)
+            ids = (restore.block_ids_per_group[group]
+                   if group < len(restore.block_ids_per_group) else ())
+            meta = lp.quant_metadata if lp is not None else {}
+            native = meta.get(_NATIVE_LAYOUT_KEY) or {}
+            if (lp is None or not ids or str(meta.get("format", lp.quantizer)) != "raw_byte_planes"
+                    or int(native.get("version", 0)) != 2):
+                rest.append((restore, fut))
+                continue
+            layout = CanonicalLayout.make(native["source_shape"], native["source_layout"],
+                                          int(native["bits"]), native.get("chunk_specs", []))
+            tokens = int(meta.get("token_count", layout.token_count // 2))
+            needed = -(-tokens // bs)
+            sizes_ok = (len(lp.chunks) == layout.num_chunks and all(
+                int(rec.unpacked_bytes) == size
+                for rec, size in zip(lp.chunks, layout.chunk_sizes())))
+            if (not sizes_ok or layout.token_count != 2 * tokens or len(ids) < needed
+                    or tuple(layout.layout) != ("token", "head", "head_dim")
+                    or layout.num_heads != H or layout.head_dim != head_bytes):
+                rest.append((restore, fut))  # the per-request path reports the error
+                continue
+            items.append((restore, fut, lp, layout, tokens, tuple(int(b) for b in ids[:needed])))
+        if len(items) < 2:
+            return rest + [(it[0], it[1]) for it in items]
+
+        key = (group, tuple(kv_cache.shape), kv_cache.dtype, kv_cache.device,
+               tuple((it[4], it[3].shape, it[3].specs.tobytes(), it[3].bits.tobytes(), it[5])
+                     for it in items))
+        batch = batches.get(key)
+        if batch is None:
+            batch = native_gpu.KVRestoreBatch(
+                [it[3] for it in items], [it[4] for it in items],
+                [np.asarray(it[5], dtype=np.int64) for it in items], kv_cache,
+                dedup_shared_blocks=True)
+            batches[key] = batch
+        bases, total = [], 0
+        for it in items:
+            bases.append(total)
+            total += -(-int(it[3].stream_bytes) // 256) * 256
+        views = [(b, int(it[3].stream_bytes)) for b, it in zip(bases, items)]
+        timed = self.metrics_path is not None
+        fill_ms: dict = {}
+
+        def fill(staging: torch.Tensor) -> None:
+            t0 = time.perf_counter()
+            comp, outs = [], []
+            for it, base in zip(items, bases):
+                lp, layout = it[2], it[3]
+                off = layout.offsets
+                for k in range(layout.num_chunks):
+                    comp.append(lp.chunks[k].compressed)
+                    outs.append(staging[base + int(off[k]):base + int(off[k + 1])])
+            self.cpu_codec.decompress_into(comp, outs)
+            fill_ms["ms"] = _ms_since(t0)
+
+        def compute(flat: torch.Tensor) -> None:
+            batch.restore([flat[b:b + n] for b, n in views], kv_cache)
+
+        with self._lease_pipeline(kv_cache.device, total) as pipe:
+            for lane in pipe.lanes:
+                batch.record_stream(lane)
+            out = pipe.submit(fill, total, compute, timed=timed)
+        results = []
+        if timed:
+            event, timing = out
+            first = items[0]
+            stream_bytes = sum(n for _, n in views)
+            written = self._written_bytes(kv_cache, sum(len(it[5]) for it in items)
+                                          - batch.skipped_blocks)
+            ids_list = [it[0].request_id for it in items]
+            self._write_restore_metric("lossless_decompress", first[0], first[2], {
+                "device": "cpu", "backend": self.cpu_codec.backend,
+                "chunks": sum(len(it[2].chunks) for it in items),
+                "compressed_bytes": sum(int(r.compressed_bytes) for it in items
+                                        for r in it[2].chunks),
+                "unpacked_bytes": stream_bytes, "ms": float(fill_ms.get("ms", 0.0)),
+                "batch_request_ids": ids_list})
+            h2d = {"bytes_copied": total, "bytes": total, "start_ts": time.time(),
+                   "device": str(kv_cache.device), "source_device": "cpu (pinned staging)",
+                   "copy_kind": "dram_to_hbm", "copy_stream": True,
+                   "batch_request_ids": ids_list,
+                   "_cuda_start_event": timing.h2d_start, "_cuda_end_event": timing.h2d_end}
+            row = {"backend": "hip_fused_unpack_scatter_batch", "batch_request_ids": ids_list,
+                   "unpacked_bytes": stream_bytes, "input_bytes": stream_bytes,
+                   "output_bytes": written, "bytes": stream_bytes + written,
+                   "shared_blocks_skipped": int(batch.skipped_blocks),
+                   "_cuda_start_event": timing.compute_start,
+                   "_cuda_end_event": timing.compute_end}
+            pending = [("h2d_copy", first[0], first[2], h2d),
+                       ("bitunpack_cuda", first[0], first[2], row)]
+            results.append(_LayerLoadResult(event=event, pending_metrics=pending))
+            results += [_LayerLoadResult(event=event) for _ in items[1:]]
+        else:
+            results = [_LayerLoadResult(event=out) for _ in items]
+        for it, result in zip(items, results):
+            self._write_restore_metric("layer_ready", it[0], it[2], {
+                "ms": _ms_since(start_perf), "chunks": len(it[2].chunks),
+                "batched_requests": len(items)})
+            it[1].set_result(result)
+        return rest
 
     def _restore_layers_in_order(self, restore: OrigamiRestoreRequest, payload: OrigamiPayload,
                                  layer_futures: dict[str, Future], start_perf: float,
@@ -293,7 +492,7 @@ class OrigamiConnectorWorker:
         timed = self.metrics_path is not None
         fill_timing: dict | None = {} if timed else None
         with self._lease_pipeline(kv_cache.device, layout.stream_bytes) as pipe:
-            ids_dev.record_stream(pipe.compute_stream)
+            pipe.record_stream(ids_dev)
             out = pipe.submit(self._fill_from_chunks(layer_payload, layout, fill_timing),
                               layout.stream_bytes, compute, timed=timed)
         if not timed:
@@ -644,6 +843,12 @@ class OrigamiConnectorWorker:
                     self._pending_request_layer_futures.pop(req_id, None)
                 finished_recving.add(req_id)
         return set(), finished_recving
+
+    def flush_metrics(self) -> None:
+        """Writes every pending event-timed metric row, waiting for its
+        events (rows are otherwise written once their layer's work is
+        observed complete)."""
+        self._flush_pending_cuda_metrics(None, final=True)
 
     def shutdown(self) -> None:
         self._executor.shutdown(wait=True)

@@ -9,7 +9,7 @@ from origami_amd.benchmark_utils import normalize_kv_value
 from origami_amd.config import OrigamiConfig
 from origami_amd.connector import KVConnectorRole, OrigamiConnector
 from origami_amd.lossless.cpu_qat import CpuLosslessCodec
-from origami_amd.metadata import OrigamiConnectorMetadata, OrigamiRestoreRequest
+from origami_amd.metadata import OrigamiConnectorMetadata, OrigamiPayload, OrigamiRestoreRequest
 from origami_amd.quantization import create_quantizer_adapter
 from origami_amd.store import InMemoryOrigamiStore, create_origami_store
 
@@ -125,3 +125,34 @@ def test_codec_threads_give_the_same_bytes():
     assert all(torch.equal(x, y) for x, y in zip(outs, data))
     with pytest.raises(RuntimeError, match="decoded"):
         many.decompress_into(b[:2], [torch.empty(5, dtype=torch.uint8), outs[1]])
+
+
+def test_batched_restore_isolates_a_failing_request():
+    """Two requests in one start_load_kv are restored by one batch task; the
+    one whose cache key is missing fails through its own futures, the other
+    (a payload with no layers to restore) completes."""
+    conn = OrigamiConnector(_vllm_config({"origami_quantizer": "raw_byte_planes",
+                                          "origami_lossless_cpu_backend": "zlib",
+                                          "origami_store_uri": "memory://cpu-batch"}),
+                            KVConnectorRole.WORKER)
+    names = ["layers.0.attn", "layers.1.attn"]
+    conn.register_kv_caches({n: torch.zeros(2, 4, 4, 1, 8) for n in names})
+    conn.connector_worker.store.put(OrigamiPayload(
+        cache_key="empty", request_id="w", quantizer="raw_byte_planes",
+        quantizer_config_hash="", token_start=0, token_count=8))
+    md = OrigamiConnectorMetadata(reqs_to_restore={
+        "bad": OrigamiRestoreRequest(request_id="bad", cache_key="missing",
+                                     block_ids_per_group=((0, 1),), num_tokens=8),
+        "ok": OrigamiRestoreRequest(request_id="ok", cache_key="empty",
+                                    block_ids_per_group=((2, 3),), num_tokens=8)})
+    conn.bind_connector_metadata(md)
+    conn.start_load_kv(None)
+    worker = conn.connector_worker
+    done = {worker._restore_future_to_request_id[f]: f for f in worker._restore_futures}
+    assert set(done) == {"bad", "ok"}
+    assert isinstance(done["bad"].exception(timeout=30), KeyError)
+    assert done["ok"].result(timeout=30) == "ok"
+    layer_futs = worker._pending_request_layer_futures["ok"]
+    assert all(f.result(timeout=30) is None for f in layer_futs)
+    with pytest.raises(KeyError):
+        conn.wait_for_layer_load(names[0])

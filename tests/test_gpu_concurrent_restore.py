@@ -1,5 +1,6 @@
 """Concurrent restores through the connector: requests of growing length in
-one batch run on separate executor threads, so a larger request replaces the
+one batch run on separate executor threads (batched restores switched off,
+origami_batch_restores), so a larger request replaces the
 device's restore pipeline while a smaller one may still be submitting to the
 old one.  Every restored block must equal the saved source block, blocks
 outside the destination tables stay zero, and the per-layer metric rows
@@ -27,7 +28,8 @@ def _connector(ns, metrics_dir=""):
             "origami_quantizer": "raw_byte_planes", "origami_lossless_cpu_backend": "zlib",
             "origami_store_uri": f"memory://{ns}", "origami_chunk_min_bytes": 1 << 16,
             "origami_chunk_target_bytes": 1 << 16, "origami_chunk_max_bytes": 1 << 16,
-            "origami_qat_threads": 8, "origami_metrics_dir": metrics_dir}))
+            "origami_qat_threads": 8, "origami_metrics_dir": metrics_dir,
+            "origami_batch_restores": False}))
     return OrigamiConnector(cfg, KVConnectorRole.WORKER)
 
 

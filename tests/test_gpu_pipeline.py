@@ -1,5 +1,6 @@
-"""Layer-wise restore pipeline: overlapped copy + fused restore gives the same
-cache bytes as the direct restore and as the oracle's unpack + scatter
+"""Layer-wise restore pipeline: overlapped copy + fused restore (layers dealt
+to 2 or 3 lane streams, each lane's slot reused every n layers) gives the
+same cache bytes as the direct restore and as the oracle's unpack + scatter
 (bitpack_layout_cuda.cu:91-128, benchmark_utils.py:350-444), from pinned
 streams and from staging fills."""
 import numpy as np
@@ -24,8 +25,9 @@ def _specs(T2, H, C, target):
                                               max_bytes=target)]
 
 
+@pytest.mark.parametrize("lanes", [2, 3])
 @pytest.mark.parametrize("mode", ["pinned", "filled"])
-def test_pipeline_matches_direct_restore(cuda_device, mode):
+def test_pipeline_matches_direct_restore(cuda_device, mode, lanes):
     g = torch.Generator().manual_seed(3)
     L, T, H, C, bs = 7, 1000, 4, 256, 16
     nblk = -(-T // bs)
@@ -45,7 +47,7 @@ def test_pipeline_matches_direct_restore(cuda_device, mode):
         oracle.restore_layer(streams[layer].numpy(), lay.offsets, 8, lay.specs, T, H, C,
                              ids_host[layer].numpy(), o)
         oracle_caches.append(o)
-    pipe = LayerRestorePipeline(cuda_device, lay.stream_bytes, num_slots=3)
+    pipe = LayerRestorePipeline(cuda_device, lay.stream_bytes, num_lanes=lanes)
     events = []
     pinned = [s.pin_memory() for s in streams]
     for layer in range(L):
