@@ -189,8 +189,13 @@ int origami_unpack_canonical_to_kv_cache(
  * table of a reordered plan is written into a fixed 1 MiB device array per
  * GPU (at most 131072 (head, channel) planes, i.e. num_heads * head_bytes;
  * larger reordered plans return ORIGAMI_ERR_UNSUPPORTED).  That array is
- * shared by every call on the GPU and keeps the last call's contents: calls
- * that overlap on one GPU (different streams or threads) race.
+ * shared by every call on the GPU and keeps the last call's contents, so
+ * reordered-plan calls on one GPU must not overlap: calls from several host
+ * threads are serialised on the host, and a call from another stream while
+ * the previous call's work is still pending returns ORIGAMI_ERR_INVALID
+ * (nothing is launched).  Inside graph capture the check is skipped; replays
+ * of captured calls must not overlap other calls on the GPU.  The device
+ * state (array address, one event) is set up on a device's first call.
  */
 int origami_unpack_canonical_to_kv_cache_noalloc(
     const uint8_t* flat_chunks, int64_t flat_bytes,

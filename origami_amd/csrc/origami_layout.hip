@@ -853,6 +853,18 @@ __device__ __forceinline__ TileIndex split_tile(const RowsParams& p, int64_t til
   return {static_cast<int>(tile % p.nst), tile / p.nst};
 }
 
+// Workgroups are dealt to the 8 XCDs round-robin (workgroup b runs on XCD
+// b mod 8), each XCD with its own L2.  xcd_run_order(i, n, run) is a
+// bijection on [0, n) that gives each XCD runs of `run` consecutive indices:
+// index i of a group of 8 * run goes to member (i / 8) mod run of XCD slot
+// i mod 8; a last partial group keeps its order.
+__device__ __forceinline__ int64_t xcd_run_order(int64_t i, int64_t n, int run) {
+  const int64_t group = 8 * static_cast<int64_t>(run);
+  if (run <= 1 || i >= n / group * group) return i;
+  const int64_t r = i % group;
+  return i - r + (r % 8) * run + r / 8;
+}
+
 // Inside a tile, whole-tile workgroups order wave tiles along channels
 // fastest; with SPLIT, workgroup `slice` holds waves [4 slice, 4 slice + 4)
 // and wave tiles run along tokens fastest, so a workgroup is one channel
@@ -1425,8 +1437,7 @@ __global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
 // The 8-bit pack off 128-byte lines (kRowsStaged8), for workgroups of WAVES
 // waves (p.waves == WAVES): LDS in proportion, so that the smaller workgroups
 // of short launches still share a CU.
-// Workgroups are dealt to the 8 XCDs round-robin (workgroup b runs on XCD
-// b mod 8), each XCD with its own L2.  The staged pack's regions share their
+// The staged pack's regions share their
 // first and last stream lines with the token-neighbouring tiles, so those
 // lines are written in two parts.  Dealing runs of kStagedXcdRun consecutive
 // token tiles to one XCD (workgroups b, b + 8, ... of a group of 8 runs) puts
@@ -1435,16 +1446,6 @@ __global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
 // 4411 / 4470; 49217 tokens 3340 / - / 3638 / 3622 / 3496; launches with
 // fewer tiles than a group (8199, 4100 tokens) unchanged.
 constexpr int kStagedXcdRun = 16;
-
-// A bijection on [0, n): index i of a group of 8 * run consecutive indices
-// goes to run member (i / 8) mod run of XCD slot i mod 8; a last partial
-// group keeps its order.
-__device__ __forceinline__ int64_t xcd_run_order(int64_t i, int64_t n, int run) {
-  const int64_t group = 8 * static_cast<int64_t>(run);
-  if (run <= 1 || i >= n / group * group) return i;
-  const int64_t r = i % group;
-  return i - r + (r % 8) * run + r / 8;
-}
 
 template <int WAVES, bool ONEBLK>
 __global__ __launch_bounds__(WAVES * 64) void rows_pack_staged8_kernel(RowsParams p) {
@@ -2237,27 +2238,86 @@ constexpr int kScratchDevices = 64;
 
 static __device__ __align__(256) int64_t scratch[kScratchPlanes];
 
-// Device address of `scratch` on the current device, looked up once per
-// device (each GPU holds its own copy of the array).  Host code must use this
-// address, never the array's name, which is only a host-side stand-in.
-int scratch_table(int64_t** out) {
-  static std::mutex mu;
-  static int64_t* ptrs[kScratchDevices] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
-    return fail(ORIGAMI_ERR_HIP, "hipGetDevice failed (or device index above 63)");
-  std::lock_guard<std::mutex> lock(mu);
-  if (ptrs[dev] == nullptr) {
-    void* p = nullptr;
-    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (err != hipSuccess || p == nullptr)
-      return fail(ORIGAMI_ERR_HIP, std::string("hipGetSymbolAddress of the restore scratch "
-                                               "table failed: ") + hipGetErrorString(err));
-    ptrs[dev] = static_cast<int64_t*>(p);
+// Per-device state of `scratch`: its device address, looked up once per
+// device (each GPU holds its own copy of the array; host code must use this
+// address, never the array's name, which is only a host-side stand-in), and
+// an event recorded after the last call that wrote it, with that call's
+// stream, so a call from another stream can see that the array is still in
+// use.  Both are set up on a device's first call.
+struct ScratchState {
+  int64_t* ptr = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool pending = false;
+};
+
+// Holds the scratch array of the current device from acquire() to its
+// destruction, under a lock, so two host threads cannot interleave their
+// table fills and launches.  acquire() refuses the array while work of a
+// call on another stream is still pending (the two would race on it); in a
+// stream that is being captured into a graph it neither checks nor records
+// (a graph's replays are ordered by the caller).
+class ScratchLease {
+ public:
+  ~ScratchLease() {
+    if (state_ && !capturing_) {
+      (void)hipEventRecord(state_->done, stream_);
+      state_->last = stream_;
+      state_->pending = true;
+    }
   }
-  *out = ptrs[dev];
-  return ORIGAMI_OK;
-}
+
+  int acquire(hipStream_t stream, int64_t** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
+      return fail(ORIGAMI_ERR_HIP, "hipGetDevice failed (or device index above 63)");
+    lock_ = std::unique_lock<std::mutex>(mutex());
+    ScratchState& st = states()[dev];
+    if (st.ptr == nullptr) {
+      void* p = nullptr;
+      const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (err != hipSuccess || p == nullptr)
+        return fail(ORIGAMI_ERR_HIP, std::string("hipGetSymbolAddress of the restore scratch "
+                                                 "table failed: ") + hipGetErrorString(err));
+      hipEvent_t ev = nullptr;
+      if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
+        return fail(ORIGAMI_ERR_HIP, "event creation for the restore scratch table failed");
+      st.ptr = static_cast<int64_t*>(p);
+      st.done = ev;
+    }
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &status) != hipSuccess)
+      return fail(ORIGAMI_ERR_HIP, "hipStreamIsCapturing failed");
+    capturing_ = status != hipStreamCaptureStatusNone;
+    if (!capturing_ && st.pending && st.last != stream) {
+      const hipError_t q = hipEventQuery(st.done);
+      if (q == hipErrorNotReady)
+        return fail(ORIGAMI_ERR_INVALID,
+                    "an allocation-free restore of a reordered chunk plan is still running on "
+                    "another stream of this GPU; such calls share one scratch plane table and "
+                    "must not overlap");
+      if (q != hipSuccess) return fail(ORIGAMI_ERR_HIP, "hipEventQuery failed");
+    }
+    state_ = &st;
+    stream_ = stream;
+    *out = st.ptr;
+    return ORIGAMI_OK;
+  }
+
+ private:
+  static std::mutex& mutex() {
+    static std::mutex mu;
+    return mu;
+  }
+  static ScratchState* states() {
+    static ScratchState s[kScratchDevices];
+    return s;
+  }
+  std::unique_lock<std::mutex> lock_;
+  ScratchState* state_ = nullptr;
+  hipStream_t stream_ = nullptr;
+  bool capturing_ = false;
+};
 
 // The PlanInfo build_plane_table would give, from the chunk list alone: O(n),
 // plus an O(n^2) box-overlap test when the chunks are not in plane order.
@@ -2683,12 +2743,18 @@ int origami_unpack_canonical_to_kv_cache_noalloc(
       return fail(ORIGAMI_ERR_UNSUPPORTED,
                   "allocation-free restore of a reordered chunk plan supports at most 131072 "
                   "(head, channel) planes (num_heads * head_bytes)");
+    // the table fill and the launch happen under the lease; its release
+    // records their completion for calls from other streams
+    ScratchLease lease;
     int64_t* table = nullptr;
-    if (int rc2 = scratch_table(&table)) return rc2;
+    if (int rc2 = lease.acquire(stream, &table)) return rc2;
     if (int rc2 = fill_plane_table(table, chunk_offsets, chunk_specs, num_chunks, 2 * tokens,
                                    num_heads, head_bytes, info.bits, stream))
       return rc2;
     p.planes = table;
+    const int mode = rows_mode(info, p, tokens, false, 0, true);
+    set_restore_grid(p, mode, info.bits, num_heads, head_bytes, p.row_tokens, 2);
+    return launch_rows(false, p, 2, info.bits, mode, stream);
   }
   const int mode = rows_mode(info, p, tokens, false, 0, true);
   set_restore_grid(p, mode, info.bits, num_heads, head_bytes, p.row_tokens, 2);

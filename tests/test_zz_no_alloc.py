@@ -5,8 +5,10 @@ second with a smaller layer), for chunk plans in the planner's order (no
 device metadata) and reordered ones (plane table in the fixed scratch
 array, rewritten by every call), at b = 8, 5 and in the wide 16-byte-run
 mode (b = 4, 2); it creates no plan and makes no device allocation; it can
-be captured in a HIP graph whose replays restore new stream contents; and
-it rejects a reordered plan above the scratch maximum."""
+be captured in a HIP graph whose replays restore new stream contents; it
+refuses a reordered-plan call from a second stream while the first
+stream's call is still pending; and it rejects a reordered plan above the
+scratch maximum."""
 import numpy as np
 import pytest
 import torch
@@ -188,3 +190,43 @@ def test_noalloc_graph_capture_replays(cuda_device, kind, bits):
         oracle.restore_layer(flat_np, offs, bits, specs, T, H, C, ids_np, expect)
         assert np.array_equal(got, expect), (kind, bits, replay)
     del graph
+
+
+def test_noalloc_refuses_overlapping_call_from_another_stream(cuda_device):
+    """A reordered-plan call queued on stream A behind a long fill, then one
+    on stream B before A has run: B's call is refused (the two would share
+    the scratch plane table); after A completes, B's call runs and matches
+    the oracle."""
+    dev = cuda_device
+    rng = np.random.default_rng(500)
+    T, H, C, bs = 640, 4, 256, 16
+    nblk = -(-T // bs)
+    NB = nblk + 3
+    specs = _specs("reordered", T, H, C, rng)
+    lay = kv_symbol_layout(T, H, C, 8, specs)
+    sym = rng.integers(0, 256, 2 * T * H * C, dtype=np.uint8)
+    flat_np, offs = oracle.pack_canonical(sym, 8, specs, [2 * T, H, C], [0, 1, 2, -1])
+    flat = torch.from_numpy(flat_np).to(dev)
+    ids_np = rng.permutation(NB)[:nblk].astype(np.int64)
+    ids = torch.from_numpy(ids_np).to(dev)
+    caches = [torch.zeros((2, NB, bs, H, C), dtype=torch.uint8, device=dev) for _ in range(2)]
+    busy = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    sa, sb = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    torch.cuda.synchronize(dev)
+    with torch.cuda.stream(sa):
+        for _ in range(20):  # ~10 ms of work ahead of A's restore
+            busy.fill_(1)
+        _restore(NOALLOC, flat, lay, T, caches[0], ids)
+    with torch.cuda.stream(sb):
+        with pytest.raises(_native.OrigamiNativeError, match="must not overlap") as err:
+            _restore(NOALLOC, flat, lay, T, caches[1], ids)
+    assert err.value.code == _native.ORIGAMI_ERR_INVALID
+    torch.cuda.synchronize(dev)
+    with torch.cuda.stream(sb):
+        _restore(NOALLOC, flat, lay, T, caches[1], ids)
+    torch.cuda.synchronize(dev)
+    expect = np.zeros(caches[0].shape, dtype=np.uint8)
+    oracle.restore_layer(flat_np, offs, 8, specs, T, H, C, ids_np, expect)
+    for c in caches:
+        assert np.array_equal(c.cpu().numpy(), expect)
+    del busy
