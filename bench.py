@@ -29,6 +29,10 @@ HBM_PEAK_GBPS = 8000.0
 METRIC = "KV restore GB/s (unpack+scatter) and % of HBM peak; per-layer restore µs"
 CAL_BYTES = 256 << 20
 
+# launch-bound single-request geometries: the configs leg adds a same-size
+# device copy beside them
+SHORT_CONFIGS = ("llama3-8b-4k", "llama3-8b-32k-tp8-rank")
+
 CONFIG_NAMES = ("llama3-8b-4k", "qwen2.5-7b-batch", "llama3-8b-fp8-16x16k", "llama3-70b-128k",
                 "llama3-8b-32k-tp8-rank")
 
@@ -676,8 +680,10 @@ def configs_leg(dev, steps, layers, only=None, min_launches=200):
       head rows), 16 requests of 16384 tokens, one batched launch per layer;
     * llama3-70b-128k: 8 KV heads, head_dim 128, bf16, one 131072-token
       request per layer;
-    * llama3-8b-4k: one layer of one 4096-token request, 8 KV heads,
-      head_dim 128, bf16, block table 0..255 (a launch-bound size);
+    * llama3-8b-4k: one 4096-token request, 8 KV heads, head_dim 128,
+      bf16, block table 0..255 (a launch-bound size); 16 layers in rotation
+      (537 MB of streams and caches), so no launch finds its layer in the
+      256 MB MALL;
     * llama3-8b-32k-tp8-rank: one tensor-parallel rank's share of the
       32768-token Llama-3-8B layer at TP = 8: 1 KV head (256-byte rows),
       head_dim 128, bf16, 16 chunks of 1 MiB per layer; 16 layers, so the
@@ -786,6 +792,22 @@ def configs_leg(dev, steps, layers, only=None, min_launches=200):
         if batch:
             ms_req = _time_passes(per_request_pass, dev, passes)
             res["per_request_us"] = round(1e3 * ms_req / nlayers, 2)
+        elif name in SHORT_CONFIGS:
+            # a device copy of the same bytes (each layer's stream into a
+            # buffer of its size), rotating over the same number of layers:
+            # what one launch of this size reaches at all
+            bufs = [torch.empty_like(reqs[0][0]) for reqs, _, _ in layers_items]
+
+            def copy_pass():
+                for (reqs, _, _), b in zip(layers_items, bufs):
+                    b.copy_(reqs[0][0])
+
+            ms_copy = _time_passes(copy_pass, dev, passes)
+            copy_bytes = 2 * layers_items[0][0][0][0].numel()
+            res["same_size_copy_us"] = round(1e3 * ms_copy / nlayers, 2)
+            res["same_size_copy_frac"] = round(
+                copy_bytes / (ms_copy / nlayers * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
+            del bufs
         if shared_pool:
             res["gbps_with_repeats"] = round(alg_repeats / (ms * 1e-3) / 1e9, 2)
             res["algorithmic_bytes_per_layer_with_repeats"] = int(alg_repeats // nlayers)
@@ -796,7 +818,7 @@ def configs_leg(dev, steps, layers, only=None, min_launches=200):
 
     geometries = {
         "llama3-8b-4k": lambda: build("llama3-8b-4k", 8, 128, torch.bfloat16, [4096], 0, False,
-                                      identity=True, nlayers=1),
+                                      identity=True, nlayers=max(layers, 16)),
         "qwen2.5-7b-batch": lambda: build(
             "qwen2.5-7b-batch", 4, 128, torch.bfloat16,
             np.random.default_rng(2).integers(8192, 65537, 8), 2, True, batch=True),
