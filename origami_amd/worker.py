@@ -319,12 +319,14 @@ class OrigamiConnectorWorker:
             sizes_ok = (len(lp.chunks) == layout.num_chunks and all(
                 int(rec.unpacked_bytes) == size
                 for rec, size in zip(lp.chunks, layout.chunk_sizes())))
+            table = tuple(int(b) for b in ids[:needed])
             if (not sizes_ok or layout.token_count != 2 * tokens or len(ids) < needed
                     or tuple(layout.layout) != ("token", "head", "head_dim")
-                    or layout.num_heads != H or layout.head_dim != head_bytes):
+                    or layout.num_heads != H or layout.head_dim != head_bytes
+                    or min(table) < 0 or max(table) >= nb):
                 rest.append((restore, fut))  # the per-request path reports the error
                 continue
-            items.append((restore, fut, lp, layout, tokens, tuple(int(b) for b in ids[:needed])))
+            items.append((restore, fut, lp, layout, tokens, table))
         if len(items) < 2:
             return rest + [(it[0], it[1]) for it in items]
 

@@ -124,3 +124,57 @@ def test_batched_restore_of_ragged_requests_with_shared_prefix(cuda_device, tmp_
         assert skipped and all(k == lead for k in skipped)
     else:
         assert backends == {"hip_fused_unpack_scatter"}
+
+
+def test_batched_restore_isolates_a_bad_block_table(cuda_device):
+    """Three requests in one start_load_kv; the second names a block id
+    outside the cache.  Its layer futures carry the error; the other two are
+    still restored by one batched launch per layer and match their saved
+    blocks."""
+    dev = cuda_device
+    rng = np.random.default_rng(33)
+    L, bs, H, D, NB = 2, 16, 4, 128, 200
+    names = [f"model.layers.{i}.self_attn.attn" for i in range(L)]
+    g = torch.Generator(device=dev).manual_seed(33)
+    src = {n: torch.randn((2, NB, bs, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+           for n in names}
+    perm = rng.permutation(NB)
+    src_tables = [perm[:30], perm[30:50], perm[50:90]]
+    saver = _connector("batch-bad")
+    saver.register_kv_caches(src)
+    saver.bind_connector_metadata(OrigamiConnectorMetadata(reqs_to_save={
+        f"s{i}": OrigamiSaveRequest(request_id=f"s{i}", cache_key=f"bk{i}",
+                                    block_ids_per_group=(tuple(int(b) for b in t),),
+                                    num_tokens=len(t) * bs)
+        for i, t in enumerate(src_tables)}))
+    saver.start_load_kv(None)
+    for n in names:
+        saver.save_kv_layer(n, src[n], None)
+    saver.wait_for_save()
+
+    perm2 = rng.permutation(NB)
+    dst_tables = [perm2[:30], perm2[30:50].copy(), perm2[50:90]]
+    dst_tables[1][7] = NB + 5  # outside the cache
+    dst = {n: torch.zeros_like(src[n]) for n in names}
+    loader = _connector("batch-bad")
+    loader.register_kv_caches(dst)
+    loader.bind_connector_metadata(OrigamiConnectorMetadata(reqs_to_restore={
+        f"r{i}": OrigamiRestoreRequest(request_id=f"r{i}", cache_key=f"bk{i}",
+                                       block_ids_per_group=(tuple(int(b) for b in t),),
+                                       num_tokens=len(t) * bs)
+        for i, t in enumerate(dst_tables)}))
+    loader.start_load_kv(None)
+    worker = loader.connector_worker
+    futs = {rid: list(f) for rid, f in worker._pending_request_layer_futures.items()}
+    for f in futs["r1"]:
+        assert f.exception(timeout=60) is not None
+    for rid in ("r0", "r2"):
+        for f in futs[rid]:
+            res = f.result(timeout=60)
+            torch.cuda.current_stream(dev).wait_event(res.event)
+    torch.cuda.synchronize(dev)
+    for n in names:
+        for i in (0, 2):
+            got = dst[n][:, dst_tables[i]].view(torch.int16)
+            assert torch.equal(got, src[n][:, src_tables[i]].view(torch.int16)), (n, i)
+    worker.shutdown()
