@@ -491,6 +491,7 @@ struct RowsParams {
   int64_t ntiles;            // workgroup tiles; a workgroup loops over tiles
   int32_t partial_last;      // the last token tile is partial: order those tiles last
   int64_t token0;            // first destination token of the tiles (a multiple of 16)
+  int32_t nt_stores;         // staged pack: whole 16-byte chunks as non-temporal stores
 };
 
 // Per-request fields of a batched restore (one layer of several requests
@@ -1278,9 +1279,11 @@ static_assert(2 * stage_round_bytes(kRowsMaxWaves) + kRowsWq * kWavePlanes * 8 <
 // Writes this lane's 16-byte chunk of region line j: stream bytes
 // [line0 + 128 j + 16 s, + 16), region bytes [o, o + 16), o = 128 j + 16 s - M
 // (M = R0 mod 128); only the bytes inside the region [0, n).  Reads at most
-// 16 bytes before and 20 after the region's bytes in LDS (its pads).
+// 16 bytes before and 20 after the region's bytes in LDS (its pads).  `nt`:
+// whole chunks as non-temporal stores (the parts of the shared edge lines stay
+// plain stores either way).
 __device__ __forceinline__ void store_region_chunk(uint8_t* line0, const uint8_t* reg, int M,
-                                                   int n, int j, int s) {
+                                                   int n, int j, int s, bool nt) {
   const int o = 128 * j + 16 * s - M;
   const int lo = o < 0 ? -o : 0, hi = n - o < 16 ? n - o : 16;
   if (lo >= hi) return;
@@ -1292,10 +1295,14 @@ __device__ __forceinline__ void store_region_chunk(uint8_t* line0, const uint8_t
   const uint32_t c2 = __builtin_amdgcn_alignbyte(w3, w2, sh);
   const uint32_t c3 = __builtin_amdgcn_alignbyte(w4, w3, sh);
   uint8_t* const dst = line0 + 128 * j + 16 * s;
-  if (lo == 0 && hi == 16)
-    *reinterpret_cast<u32x4*>(dst) = u32x4{c0, c1, c2, c3};
-  else
+  if (lo == 0 && hi == 16) {
+    if (nt)
+      __builtin_nontemporal_store(u32x4{c0, c1, c2, c3}, reinterpret_cast<u32x4*>(dst));
+    else
+      *reinterpret_cast<u32x4*>(dst) = u32x4{c0, c1, c2, c3};
+  } else {
     store_chunk_part(dst, c0, c1, c2, c3, lo, hi);
+  }
 }
 
 // Every wave of the workgroup runs this for every tile (no early exit: the
@@ -1339,10 +1346,11 @@ __device__ __forceinline__ void pack_tile_staged8(const RowsParams& p, TileIndex
       uint8_t* const r0 = p.stream + ((d + p.bit_bias + sym0 * 8) >> 3);
       const int M = static_cast<int>(reinterpret_cast<uintptr_t>(r0) & 127);
       const uint8_t* const reg = buf + (kk * slots + tc.slot) * RS + kStageFront;
-      store_region_chunk(r0 - M, reg, M, n, wsi, s);
+      const bool nt = p.nt_stores != 0;
+      store_region_chunk(r0 - M, reg, M, n, wsi, s, nt);
       // the line past the waves' own (when the region is off a line): one
       // wave per plane, a different one for each plane
-      if (wsi == (k & (p.ws - 1))) store_region_chunk(r0 - M, reg, M, n, p.ws, s);
+      if (wsi == (k & (p.ws - 1))) store_region_chunk(r0 - M, reg, M, n, p.ws, s, nt);
     });
   });
 }
@@ -1446,6 +1454,7 @@ __global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
 // 4411 / 4470; 49217 tokens 3340 / - / 3638 / 3622 / 3496; launches with
 // fewer tiles than a group (8199, 4100 tokens) unchanged.
 constexpr int kStagedXcdRun = 16;
+constexpr int kStagedNtTiles = 4;
 
 template <int WAVES, bool ONEBLK>
 __global__ __launch_bounds__(WAVES * 64) void rows_pack_staged8_kernel(RowsParams p) {
@@ -2134,6 +2143,13 @@ int launch_rows(bool pack, const RowsParams& params, int64_t nhalf, int bits, in
   }
   if (staged) {
     if (!pack || bits != 8) return fail(ORIGAMI_ERR_INVALID, "staged rows mode is the 8-bit pack");
+    // Non-temporal chunk stores below kStagedNtTiles tiles per CU.  Pack
+    // GB/s, plain -> non-temporal (same box, two runs each): 4100 tokens
+    // 1696 / 1697 -> 1802 / 1762, 8199: 2368 / 2366 -> 2584 / 2606, 16383:
+    // 4429 / 4375 -> 4637 / 4795, 32753: 4292 / 4303 -> 4308 / 4333, 49217:
+    // 3638 / 3645 -> 3766 / 3776; 65521 tokens (4 tiles per CU): 4203 / 4201
+    // -> 4135 / 4119.
+    p.nt_stores = p.ntiles < kStagedNtTiles * static_cast<int64_t>(device_cu_count());
     if (p.waves == 16)
       launch_staged_tiles<16>(grid, block, stream, p, oneblk);
     else if (p.waves == 8)

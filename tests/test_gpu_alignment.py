@@ -42,7 +42,8 @@ def _oracle_threads():
     40000,   # planes 64 bytes off, partial last tile
     49216,   # planes on lines, V half off, partial last tile
     3088,    # small: 4-wave tiles, partial last tile
-    32753,   # odd: runs at any byte; staged pack in 16-wave tiles
+    32753,   # odd: runs at any byte; staged pack in 16-wave tiles, non-temporal stores
+    65521,   # odd: staged pack at 4 tiles per CU, plain stores
     16383,   # odd: staged pack in 16-wave tiles, one per CU
     4100,    # staged pack in 8-wave tiles, 4-token last tile
     2053,    # staged pack in 4-wave tiles
