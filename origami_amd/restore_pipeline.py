@@ -106,6 +106,17 @@ def lane_streams(device: torch.device, count: int) -> list[torch.cuda.Stream]:
         return lanes[:count]
 
 
+def order_lanes_after(stream: torch.cuda.Stream, count: int) -> None:
+    """Makes the first `count` lane streams of `stream`'s device wait for the
+    work queued on `stream` so far.  The reference restores on the calling
+    thread's current stream (worker.py:1087-1248), after everything queued
+    there before; a restore issued after this call is ordered the same way
+    (for instance after kernels of an earlier step that still read the
+    blocks it overwrites)."""
+    for lane in lane_streams(stream.device, max(2, int(count))):
+        lane.wait_stream(stream)
+
+
 class LayerRestorePipeline:
     """Copy-overlapped restore of one layer at a time into a cache, on
     `num_lanes` lane streams."""

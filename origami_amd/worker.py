@@ -53,7 +53,8 @@ from origami_amd.metadata import (
 )
 from origami_amd.quantization import QuantizerAdapter, create_quantizer_adapter
 from origami_amd.quantization.raw_tensor import RawBytePlanesAdapter
-from origami_amd.restore_pipeline import LayerRestorePipeline, PipelineRegistry
+from origami_amd.restore_pipeline import (LayerRestorePipeline, PipelineRegistry,
+                                          order_lanes_after)
 from origami_amd.store import OrigamiStore
 
 _NATIVE_LAYOUT_KEY = "origami_native_layout"
@@ -166,6 +167,11 @@ class OrigamiConnectorWorker:
         if not metadata.reqs_to_restore:
             return
         restores = list(metadata.reqs_to_restore.values())
+        # restores run on the pipelines' lane streams: order them after the
+        # work already queued on this thread's current stream, as a restore
+        # on that stream would be (worker.py:1087-1248)
+        for device in {t.device for t in self.kv_caches.values() if t.is_cuda}:
+            order_lanes_after(torch.cuda.current_stream(device), self.config.restore_slots)
         write_jsonl(self.metrics_path, {
             "type": "restore_batch_meta", "system": "origami", "restore_count": len(restores),
             "request_ids": [r.request_id for r in restores],

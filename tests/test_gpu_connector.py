@@ -172,3 +172,55 @@ def test_save_then_restore_through_file_store(cuda_device, tmp_path, quantizer):
             adapter.dequantize(blob.to(cuda_device), lp.quant_metadata, dst_cache=ref[n],
                                block_ids=dst_ids).synchronize()
             assert torch.equal(dst[n].view(torch.int16), ref[n].view(torch.int16)), n
+
+
+def test_restore_waits_for_work_queued_before_start_load_kv(cuda_device):
+    """Restores run on the layer pipeline's own streams; start_load_kv orders
+    them after the work already queued on the caller's current stream, as the
+    reference's restore on that stream is (worker.py:1087-1248).  Here that
+    work is a delayed overwrite of the destination cache: the restored bytes
+    must be what is left afterwards.  (The block-table uploads from pageable
+    memory on the worker thread's stream also wait for that work today; the
+    explicit order keeps the result independent of them.)"""
+    g = torch.Generator(device=cuda_device).manual_seed(11)
+    L, NB, bs, H, D, nblk = 2, 64, 16, 8, 128, 40
+    names = [f"model.layers.{i}.self_attn.attn" for i in range(L)]
+    src = {n: torch.randn((2, NB, bs, H, D), generator=g, device=cuda_device,
+                          dtype=torch.bfloat16) for n in names}
+    src_ids = torch.randperm(NB, generator=g, device=cuda_device)[:nblk].tolist()
+    saver = _connector("raw_byte_planes", "ordered")
+    saver.register_kv_caches(src)
+    saver.bind_connector_metadata(OrigamiConnectorMetadata(reqs_to_save={
+        "s": OrigamiSaveRequest(request_id="s", cache_key="ck",
+                                block_ids_per_group=(tuple(src_ids),), num_tokens=nblk * bs)}))
+    saver.start_load_kv(None)
+    for n in names:
+        saver.save_kv_layer(n, src[n], None)
+    saver.wait_for_save()
+
+    dst = {n: torch.zeros_like(src[n]) for n in names}
+    dst_ids = torch.randperm(NB, generator=g, device=cuda_device)[:nblk].tolist()
+    loader = _connector("raw_byte_planes", "ordered")
+    loader.register_kv_caches(dst)
+    torch.cuda.synchronize()
+    # the caller's stream: a bounded spin of about half a second (calibrated
+    # with events), then an overwrite of every block
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    torch.cuda._sleep(1 << 22)
+    end.record()
+    end.synchronize()
+    ms_per_cycle = max(start.elapsed_time(end), 1e-3) / (1 << 22)
+    torch.cuda._sleep(int(min(500.0 / ms_per_cycle, 1e11)))
+    for n in names:
+        dst[n].fill_(3.0)
+    loader.bind_connector_metadata(OrigamiConnectorMetadata(reqs_to_restore={
+        "r": OrigamiRestoreRequest(request_id="r", cache_key="ck",
+                                   block_ids_per_group=(tuple(dst_ids),), num_tokens=nblk * bs)}))
+    loader.start_load_kv(None)
+    for n in names:
+        loader.wait_for_layer_load(n)
+    torch.cuda.synchronize()
+    for n in names:
+        assert torch.equal(dst[n][:, dst_ids].view(torch.int16),
+                           src[n][:, src_ids].view(torch.int16)), n
