@@ -1334,6 +1334,8 @@ def cpu_baseline(stream, layout, specs, T, H, C, bs, NB, ids, restored_cache, la
                    f"median of {reps}"),
         "ms_per_layer": legs[0]["ms_per_layer"],
         "cpu_model": _host_cpu_model(),
+        "host_cpus": os.cpu_count(),
+        "cpus_usable": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
         "matches_gpu": all(leg.get("matches_gpu", True) for leg in legs),
         "legs": legs,
     }
