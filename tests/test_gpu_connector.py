@@ -81,7 +81,7 @@ def test_save_then_restore_through_connector(cuda_device, quantizer, blocks_firs
         want = _gather(src[n], src_ids, blocks_first)
         assert torch.equal(got.view(torch.int16), want.view(torch.int16)), n
     finished = set()
-    for _ in range(200):
+    for _ in range(500):
         finished |= loader.get_finished(set())[1]
         if finished:
             break

@@ -173,7 +173,7 @@ def test_quantized_save_restore_through_connector(cuda_device, quantizer, extra)
         err = (dst[n][:, dst_ids].float() - src[n][:, src_ids].float()).abs()
         assert float(err.mean()) < float(src[n][:, src_ids].float().abs().mean()) * 0.9
     finished = set()
-    for _ in range(200):
+    for _ in range(500):
         finished |= loader.get_finished(set())[1]
         if finished:
             break

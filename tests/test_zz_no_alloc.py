@@ -193,7 +193,7 @@ def test_noalloc_graph_capture_replays(cuda_device, kind, bits):
 
 
 def test_noalloc_refuses_overlapping_call_from_another_stream(cuda_device):
-    """A reordered-plan call queued on stream A behind a long fill, then one
+    """A reordered-plan call queued on stream A behind a long spin, then one
     on stream B before A has run: B's call is refused (the two would share
     the scratch plane table); after A completes, B's call runs and matches
     the oracle."""
@@ -210,12 +210,18 @@ def test_noalloc_refuses_overlapping_call_from_another_stream(cuda_device):
     ids_np = rng.permutation(NB)[:nblk].astype(np.int64)
     ids = torch.from_numpy(ids_np).to(dev)
     caches = [torch.zeros((2, NB, bs, H, C), dtype=torch.uint8, device=dev) for _ in range(2)]
-    busy = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     sa, sb = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
     torch.cuda.synchronize(dev)
+    # a bounded spin of about 200 ms (calibrated with events) ahead of A's
+    # restore, so A is still pending when B's call comes, whatever the host does
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    torch.cuda._sleep(1 << 22)
+    end.record()
+    end.synchronize()
+    ms_per_cycle = max(start.elapsed_time(end), 1e-3) / (1 << 22)
     with torch.cuda.stream(sa):
-        for _ in range(20):  # ~10 ms of work ahead of A's restore
-            busy.fill_(1)
+        torch.cuda._sleep(int(min(200.0 / ms_per_cycle, 4e10)))
         _restore(NOALLOC, flat, lay, T, caches[0], ids)
     with torch.cuda.stream(sb):
         with pytest.raises(_native.OrigamiNativeError, match="must not overlap") as err:
@@ -229,4 +235,3 @@ def test_noalloc_refuses_overlapping_call_from_another_stream(cuda_device):
     oracle.restore_layer(flat_np, offs, 8, specs, T, H, C, ids_np, expect)
     for c in caches:
         assert np.array_equal(c.cpu().numpy(), expect)
-    del busy
