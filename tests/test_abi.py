@@ -58,6 +58,13 @@ def test_validation_accepts_planner_layout():
     (dict(shape=[10, 1, 8, 2], axes=[0, 1, 2, 3]), "layer axis size 1"),
     (dict(T=11), "token axis size"),
     (dict(axes=[0, 0, 2, -1]), "axes must be unique|head axis size"),
+    (dict(T=0, shape=[0, 1, 8]), "shape must be positive"),
+    (dict(shape=[10, 0, 8]), "must be positive"),
+    (dict(specs=[[0, 1, 0, 4, 0, 11], [0, 1, 4, 8, 0, 10]]), "token range"),
+    (dict(specs=[[0, 1, 4, 4, 0, 10], [0, 1, 4, 8, 0, 10]]), "channel range"),
+    (dict(offsets=[-40, 0, 40]), "non-negative"),
+    (dict(bits=[8, 9]), "1..8 bit"),
+    (dict(axes=[0, 1, 5, -1]), "head_dim axis must be present"),
 ])
 def test_validation_messages(mutate, msg):
     args = dict(offsets=[0, 40, 80], bits=[8, 8],
