@@ -164,6 +164,37 @@ def test_save_from_kv_cache_matches_oracle(cuda_device, tokens, H, C, bs, blocks
 
 
 @pytest.mark.parametrize("blocks_first", [False, True])
+@pytest.mark.parametrize("bits", [8, 5, 3, 1])
+@pytest.mark.parametrize("tokens,bs", [(1, 16), (2, 8), (7, 16), (15, 16), (17, 8)])
+def test_tiny_token_counts_restore_and_save(cuda_device, tokens, bs, blocks_first, bits):
+    """Token counts below or just past one lane's 16-token run: every lane
+    run is the partial last one of its half, planes are a few bytes long
+    (chunks of 16 bytes), and the stream ends inside most runs.  The restore
+    into a cache of random bytes and the save from it both equal the oracle."""
+    H, C = 2, 32
+    rng = np.random.default_rng(tokens * 11 + bits + bs)
+    specs = planner_specs(2 * tokens, H, C, 16)
+    value = rng.integers(0, 256, (2, tokens, H, C), dtype=np.uint8)
+    flat, offs = oracle.pack_canonical(value.reshape(-1), bits, specs, [2 * tokens, H, C],
+                                       [0, 1, 2, -1])
+    ids, cache = _kv_case(rng, tokens, H, C, bs, blocks_first)
+    expect = cache.copy()
+    oracle.restore_layer(flat, offs, bits, specs, tokens, H, C, ids, expect, blocks_first)
+    lay = kv_symbol_layout(tokens, H, C, bits, specs)
+    nb = cache.shape[0 if blocks_first else 1]
+    cache_gpu = _gpu_u8(cache, cuda_device)
+    ids_gpu = native_gpu.block_ids_tensor(ids, cuda_device, nb)
+    native_gpu.unpack_to_kv_cache(_gpu_u8(flat, cuda_device), lay, tokens, cache_gpu, ids_gpu)
+    assert np.array_equal(cache_gpu.cpu().numpy(), expect), "restore"
+
+    gathered = oracle.gather_kv_cache(cache, ids, blocks_first).reshape(2, ids.size * bs, H, C)
+    sym = np.ascontiguousarray(gathered[:, :tokens]).reshape(-1)
+    ref, _ = oracle.pack_canonical(sym, bits, specs, [2 * tokens, H, C], [0, 1, 2, -1])
+    packed = native_gpu.pack_from_kv_cache(_gpu_u8(cache, cuda_device), ids_gpu, tokens, lay)
+    assert np.array_equal(packed.cpu().numpy(), ref), "save"
+
+
+@pytest.mark.parametrize("blocks_first", [False, True])
 @pytest.mark.parametrize("bits", [8, 4])
 @pytest.mark.parametrize("tokens", [16384, 8192])
 def test_smaller_workgroups_restore_and_save(cuda_device, tokens, bits, blocks_first):
