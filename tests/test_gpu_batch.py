@@ -96,6 +96,18 @@ def test_batch_more_requests_than_one_launch(cuda_device):
     _run(cuda_device, rng, lengths, 8, 128, 8, 16, False, 0.0, False)
 
 
+@pytest.mark.parametrize("bits", [8, 5, 1])
+@pytest.mark.parametrize("blocks_first", [False, True])
+def test_batch_tiny_requests(cuda_device, bits, blocks_first):
+    """Requests of 1 to 33 tokens (every lane run partial or the stream ending
+    inside it) beside one of 1500, in one batch, with and without a shared
+    prefix of whole blocks."""
+    rng = np.random.default_rng(70 + bits + int(blocks_first))
+    lengths = [1, 5, 15, 16, 17, 33, 1500]
+    _run(cuda_device, rng, lengths, 2, 64, bits, 16, blocks_first, 0.0, False)
+    _run(cuda_device, rng, [32, 33, 48, 1500], 2, 64, bits, 16, blocks_first, 0.5, True)
+
+
 @pytest.mark.parametrize("bs,blocks_first", [(32, True), (8, False), (16, True)])
 def test_batch_block_sizes_and_layouts(cuda_device, bs, blocks_first):
     rng = np.random.default_rng(bs + int(blocks_first))
