@@ -48,6 +48,9 @@ def _specs(kind, T, H, C, rng, target=1 << 14):
     ("planner", 2048, 1, 16, True),
     ("planner", 2048, 2, 24, False),
     ("reordered", 1024, 4, 8, False),
+    # fewer tokens than one lane run
+    ("planner", 7, 8, 16, False),
+    ("reordered", 15, 3, 8, True),
 ])
 def test_prepared_restore_matches_fused_and_oracle(cuda_device, kind, T, bits, bs,
                                                    blocks_first):

@@ -80,9 +80,11 @@ def _case(dev, rng, kind, T, H, C, bits, bs, blocks_first):
 @pytest.mark.parametrize("bits", [8, 5])
 def test_noalloc_matches_fused_restore_twice(cuda_device, kind, bits):
     rng = np.random.default_rng(100 + bits)
-    # first call, then a smaller layer (fewer tokens, heads and channels)
+    # first call, then a smaller layer (fewer tokens, heads and channels),
+    # then one of 7 tokens (a single partial lane run per half)
     _case(cuda_device, rng, kind, 1000, 8, 256, bits, 16, False)
     _case(cuda_device, rng, kind, 300, 4, 128, bits, 16, True)
+    _case(cuda_device, rng, kind, 7, 2, 32, bits, 16, False)
 
 
 def test_noalloc_alternating_plans_rewrite_scratch(cuda_device):
