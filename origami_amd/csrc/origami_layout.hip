@@ -492,6 +492,7 @@ struct RowsParams {
   int32_t partial_last;      // the last token tile is partial: order those tiles last
   int64_t token0;            // first destination token of the tiles (a multiple of 16)
   int32_t nt_stores;         // staged pack: whole 16-byte chunks as non-temporal stores
+  int32_t own_lines;         // staged pack: each stream line written by one tile (16 waves)
 };
 
 // Per-request fields of a batched restore (one layer of several requests
@@ -1355,6 +1356,116 @@ __device__ __forceinline__ void pack_tile_staged8(const RowsParams& p, TileIndex
   });
 }
 
+// Single-owner variant of the staged pack (own_lines, 16-wave tiles).  A tile
+// holds kOwnTokens = 15 * 128 tokens of its half, [T0, T0 + n); wave 0
+// gathers the 128 tokens before T0 as well (the K half's last 128 for the V
+// half's first tile), so that the LDS region reg[i] holds the plane byte of
+// token T0 - 128 + i, i in [0, 2048).  In the stream a plane's region starts
+// M = R0 mod 128 bytes into its first line; the tile writes every line whose
+// last byte is in its region, whole, the M bytes before R0 included, and
+// leaves the line holding its region's end to the tile after it.  So each
+// stream line is written by one tile in one piece, except the two lines at
+// each plane's start and end, whose other bytes belong to another plane:
+// there the tile writes its own bytes only, as the two-part scheme does.
+// Against writing a region's first and last lines in two parts (one by each
+// neighbouring tile), a timing-only copy of the kernel with every line written
+// once and whole took 57.1-57.4 against 61.5-61.8 us per 32753-token layer.
+constexpr int kOwnTokens = 15 * 128;
+
+// Writes the bytes [a, b) of this lane's chunk s of line j (offsets from the
+// line's start line0, a plane's region starting M bytes into line 0): stream
+// bytes [line0 + 128 j + 16 s, + 16) from LDS bytes reg[128 - M + 128 j + 16 s
+// ...] (5 dwords read, at most 20 bytes past the chunk).
+__device__ __forceinline__ void store_owned_chunk(uint8_t* line0, const uint8_t* reg, int M,
+                                                  int j, int s, int a, int b, bool nt) {
+  const int o = 128 * j + 16 * s;
+  const int lo = a > o ? a - o : 0, hi = b - o < 16 ? b - o : 16;
+  if (lo >= hi) return;
+  const int i = 128 - M + o;
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(reg + (i & ~3));
+  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
+  const uint32_t sh = static_cast<uint32_t>(i & 3);
+  const uint32_t c0 = __builtin_amdgcn_alignbyte(w1, w0, sh);
+  const uint32_t c1 = __builtin_amdgcn_alignbyte(w2, w1, sh);
+  const uint32_t c2 = __builtin_amdgcn_alignbyte(w3, w2, sh);
+  const uint32_t c3 = __builtin_amdgcn_alignbyte(w4, w3, sh);
+  uint8_t* const dst = line0 + o;
+  if (lo == 0 && hi == 16) {
+    if (nt)
+      __builtin_nontemporal_store(u32x4{c0, c1, c2, c3}, reinterpret_cast<u32x4*>(dst));
+    else
+      *reinterpret_cast<u32x4*>(dst) = u32x4{c0, c1, c2, c3};
+  } else {
+    store_chunk_part(dst, c0, c1, c2, c3, lo, hi);
+  }
+}
+
+// pack_tile_staged8 with own_lines: every wave of the workgroup runs this for
+// every tile (the rounds hold barriers).  p.T >= 128 (the V half's first tile
+// reads the K half's last 128 tokens, whose runs start at any token, so rows
+// are gathered through the block-table walk; 16-wave staged tiles only run at
+// 8 or more waves per CU, where the walk is the faster order anyway).
+__device__ __forceinline__ void pack_tile_owned(const RowsParams& p, TileIndex ti,
+                                                const int64_t* desc, uint8_t* stage) {
+  constexpr int WAVES = 16;
+  TileCoord tc = tile_coord(p, ti);
+  const int s = static_cast<int>(threadIdx.x & 7);
+  const int wsi = static_cast<int>(threadIdx.x >> 6);  // wq == 1: the wave's token row
+  const int64_t T0 = static_cast<int64_t>(ti.st) * kOwnTokens;
+  const bool slot_ok = tc.q < p.nq;
+  const bool kv_halo = tc.half == 1 && T0 == 0;  // wave 0 reads the K half's tail
+  tc.t0 = T0 - 128 + (static_cast<int64_t>(wsi) * kLaneSegs + s) * kSegTokens;
+  int nv = 0;
+  if (wsi == 0) {
+    if (kv_halo) {
+      tc.half = 0;
+      tc.t0 += p.T;
+    }
+    if (slot_ok && (T0 > 0 || kv_halo)) nv = 16;
+  } else if (slot_ok && tc.t0 < p.T) {
+    nv = static_cast<int>(p.T - tc.t0 < 16 ? p.T - tc.t0 : 16);
+  }
+
+  uint32_t r[16][4];
+  load_tile_rows<false>(p, tc, nv, r);
+  uint32_t v[16][4];
+  transpose16(r, v);
+
+  const int64_t half = kv_halo ? 1 : tc.half;
+  const int n = static_cast<int>(p.T - T0 < kOwnTokens ? p.T - T0 : kOwnTokens);
+  const bool first_part = half == 0 && T0 == 0;         // the plane's first line
+  const bool last_part = half == 1 && T0 + n == p.T;    // the plane's last line
+  const int RS = WAVES * 128 + kStageFront + kStageBack;
+  const int slots = p.wq * kLaneGroups;
+  const int64_t sym0 = half * p.T + T0;
+  const int run_off = kStageFront + (wsi * kLaneSegs + s) * kSegTokens;
+  const bool nt = p.nt_stores != 0;
+  static_for<16 / kStagePlanes>([&](auto rc) {
+    constexpr int round = decltype(rc)::value;
+    uint8_t* const buf = stage + (round & 1) * stage_round_bytes(WAVES);
+    static_for<kStagePlanes>([&](auto kc) {
+      constexpr int kk = decltype(kc)::value, k = round * kStagePlanes + kk;
+      if (nv > 0 && desc[tc.slot * 16 + k] >= 0)
+        *reinterpret_cast<u32x4*>(buf + (kk * slots + tc.slot) * RS + run_off) =
+            u32x4{v[k][0], v[k][1], v[k][2], v[k][3]};
+    });
+    __syncthreads();
+    static_for<kStagePlanes>([&](auto kc) {
+      constexpr int kk = decltype(kc)::value, k = round * kStagePlanes + kk;
+      const int64_t d = desc[tc.slot * 16 + k];
+      if (!slot_ok || d < 0) return;
+      uint8_t* const r0 = p.stream + ((d + p.bit_bias + sym0 * 8) >> 3);
+      const int M = static_cast<int>(reinterpret_cast<uintptr_t>(r0) & 127);
+      const uint8_t* const reg = buf + (kk * slots + tc.slot) * RS + kStageFront;
+      // bytes [a, b) from the region's first line: whole lines up to the
+      // last one that ends inside the region, the plane's ends only in part
+      const int a = first_part ? M : 0;
+      const int b = last_part ? M + n : 128 * ((M + n) >> 7);
+      store_owned_chunk(r0 - M, reg, M, wsi, s, a, b, nt);
+    });
+  });
+}
+
 // Writes the low `nbits` bits (> 0) of u[] into the stream at bit P
 // (kRowsBits).  The 8 lanes of a group hold consecutive runs of one plane,
 // lane i at P0 + 16 b i, and the group's bits are [P0, Pend).  A dword wholly
@@ -1456,15 +1567,19 @@ __global__ __launch_bounds__(kRowsThreads) void rows_pack_kernel(RowsParams p) {
 constexpr int kStagedXcdRun = 16;
 constexpr int kStagedNtTiles = 4;
 
-template <int WAVES, bool ONEBLK>
+template <int WAVES, bool ONEBLK, bool OWN = false>
 __global__ __launch_bounds__(WAVES * 64) void rows_pack_staged8_kernel(RowsParams p) {
+  static_assert(!OWN || (WAVES == 16 && !ONEBLK), "single-owner tiles: 16 waves, row walk");
   __shared__ int64_t desc[kRowsWq * kWavePlanes];
   __shared__ __align__(16) uint8_t stage[2 * stage_round_bytes(WAVES)];
   for (int64_t t = blockIdx.x; t < p.ntiles; t += gridDim.x) {
     const int64_t tile = xcd_run_order(t, p.ntiles, kStagedXcdRun);
     const TileIndex ti = split_tile(p, tile);
     load_descriptors(p, ti, desc);
-    pack_tile_staged8<WAVES, ONEBLK>(p, ti, desc, stage);
+    if constexpr (OWN)
+      pack_tile_owned(p, ti, desc, stage);
+    else
+      pack_tile_staged8<WAVES, ONEBLK>(p, ti, desc, stage);
   }
 }
 
@@ -1992,11 +2107,30 @@ constexpr int kStagedWq = 1;
 // 2315 / 2482, 15000 tokens 3235 / 3565 / 3824; at 2053 tokens 4-wave tiles
 // stay fastest (955 against 901 / 699).
 void set_pack_grid(RowsParams& p, int mode, int64_t H, int64_t C, int64_t T, int64_t nhalf) {
-  if (mode == kRowsStaged8)
+  p.own_lines = 0;
+  if (mode == kRowsStaged8) {
     set_grid_dims(p, H, C, T, nhalf, kStagedWq, kSegTokens, kRowsMaxWaves,
                   std::max<int64_t>(1, device_cu_count() / 2));
-  else
+    // 16-wave tiles write each stream line from one tile (kOwnTokens per
+    // tile) when that takes no more rounds of tiles per CU (one 16-wave tile
+    // per CU at a time): the smaller tiles are more of them, and a further
+    // round cost more than single ownership saves.  µs per layer, two-part
+    // lines -> single owner: 49217 tokens 111.0 -> 103.4 (4 rounds either
+    // way); 32753 tokens 62.9 -> 73.3 and 16383 tokens 30.5 -> 46.5 (2 -> 3
+    // and 1 -> 2 rounds: not taken).
+    if (p.waves == 16 && p.wq == 1 && T >= 128 && nhalf == 2) {
+      const int64_t nst_own = (T + kOwnTokens - 1) / kOwnTokens;
+      const int64_t per_st = nhalf * p.H * static_cast<int64_t>(p.nqt);
+      const int64_t cus = device_cu_count();
+      if ((per_st * nst_own + cus - 1) / cus <= (per_st * p.nst + cus - 1) / cus) {
+        p.own_lines = 1;
+        p.nst = static_cast<int32_t>(nst_own);
+        p.partial_last = 0;
+      }
+    }
+  } else {
     set_grid_dims(p, H, C, T, nhalf);
+  }
 }
 
 template <int BITS, int MODE>
@@ -2026,6 +2160,12 @@ void launch_pack_tiles(dim3 grid, dim3 block, hipStream_t stream, const RowsPara
 template <int WAVES>
 void launch_staged_tiles(dim3 grid, dim3 block, hipStream_t stream, const RowsParams& p,
                          bool oneblk) {
+  if constexpr (WAVES == 16) {
+    if (p.own_lines) {  // the row walk whatever `oneblk` says (pack_tile_owned)
+      hipLaunchKernelGGL((rows_pack_staged8_kernel<16, false, true>), grid, block, 0, stream, p);
+      return;
+    }
+  }
   if (oneblk)
     hipLaunchKernelGGL((rows_pack_staged8_kernel<WAVES, true>), grid, block, 0, stream, p);
   else

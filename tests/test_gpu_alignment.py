@@ -44,6 +44,9 @@ def _oracle_threads():
     3088,    # small: 4-wave tiles, partial last tile
     32753,   # odd: runs at any byte; staged pack in 16-wave tiles, non-temporal stores
     65521,   # odd: staged pack at 4 tiles per CU, plain stores
+    12001,   # odd: staged pack, each stream line written by one tile (1 round)
+    24001,   # the same over 2 rounds of tiles
+    49217,   # the same over 4 rounds of tiles
     16383,   # odd: staged pack in 16-wave tiles, one per CU
     4100,    # staged pack in 8-wave tiles, 4-token last tile
     2053,    # staged pack in 4-wave tiles
@@ -90,12 +93,13 @@ def test_byte_planes_off_lines(cuda_device, T, blocks_first):
 
 
 @pytest.mark.parametrize("shift", [5, 16, 77])
-def test_staged_pack_into_offset_stream(cuda_device, shift):
-    """The staged 8-bit pack of a full 32753-token layer (16-wave workgroups)
-    written `shift` bytes into a larger buffer: the stream equals the oracle's
-    and the bytes around it keep their guard value (the lines at the
-    stream's ends are partial)."""
-    dev, C, T = cuda_device, D * 2, 32753
+@pytest.mark.parametrize("T", [32753, 24001])
+def test_staged_pack_into_offset_stream(cuda_device, shift, T):
+    """The staged 8-bit pack of a full layer (16-wave workgroups; at 24001
+    tokens each stream line is written by one tile) written `shift` bytes
+    into a larger buffer: the stream equals the oracle's and the bytes around
+    it keep their guard value (the lines at the stream's ends are partial)."""
+    dev, C = cuda_device, D * 2
     gen = torch.Generator(device=dev)
     gen.manual_seed(shift)
     nblk = -(-T // BS)
