@@ -123,3 +123,41 @@ def test_staged_pack_into_offset_stream(cuda_device, shift, T):
     assert np.array_equal(host[shift:shift + lay.stream_bytes], flat), "pack differs from the oracle"
     assert (host[:shift] == 0xA5).all() and (host[shift + lay.stream_bytes:] == 0xA5).all(), \
         "bytes outside the stream were written"
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_staged_pack_random_geometries(cuda_device, seed):
+    """Seeded staged packs at 5000-60000 odd token counts, 2-8 heads of 128
+    or 256 bytes, block size 16 or 32, both cache layouts and an output
+    pointer 0-64 bytes into its buffer.  Most of these draws take 16-wave
+    tiles in which each stream line is written by one tile.  The stream
+    equals the oracle's and the bytes around it keep their guard value."""
+    dev = cuda_device
+    rng = np.random.default_rng(900 + seed)
+    T = int(rng.integers(5000, 60000)) | 1
+    H = int(rng.choice([2, 4, 8]))
+    C = int(rng.choice([128, 256]))
+    bs = int(rng.choice([16, 32]))
+    blocks_first = bool(rng.integers(0, 2))
+    shift = int(rng.choice([0, 3, 64]))
+    nblk = -(-T // bs)
+    NB = nblk + 9
+    shape = (NB, 2, bs, H, C) if blocks_first else (2, NB, bs, H, C)
+    src = torch.from_numpy(rng.integers(0, 256, shape, dtype=np.uint8)).to(dev)
+    st = rng.permutation(NB)[:nblk].astype(np.int64)
+    plan = plan_head_channel_chunks(layer_index=0, num_heads=H, head_dim=C, token_count=2 * T,
+                                    bytes_per_symbol=1, min_bytes=1 << 20,
+                                    target_bytes=1 << 20, max_bytes=1 << 20)
+    specs = [[c.layout.head_start, c.layout.head_end, c.layout.channel_start,
+              c.layout.channel_end, c.layout.token_start, c.layout.token_end] for c in plan]
+    lay = kv_symbol_layout(T, H, C, 8, specs)
+    buf = torch.full((lay.stream_bytes + shift + 131,), 0xA5, dtype=torch.uint8, device=dev)
+    native_gpu.pack_from_kv_cache(src, native_gpu.block_ids_tensor(st, dev, NB), T, lay,
+                                  buf[shift:shift + lay.stream_bytes])
+    host = buf.cpu().numpy()
+    sym = oracle.gather_kv_cache(src.cpu().numpy(), st, blocks_first=blocks_first)
+    sym = sym.reshape(2, -1, H, C)[:, :T].reshape(-1)
+    flat, _ = oracle.pack_canonical(sym, 8, specs, [2 * T, H, C], [0, 1, 2, -1])
+    case = (T, H, C, bs, blocks_first, shift)
+    assert np.array_equal(host[shift:shift + lay.stream_bytes], flat), case
+    assert (host[:shift] == 0xA5).all() and (host[shift + lay.stream_bytes:] == 0xA5).all(), case
