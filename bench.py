@@ -291,6 +291,9 @@ def main() -> int:
 
     if not args.no_pack_ragged:
         result["pack_ragged"] = pack_ragged_leg(dev, max(3, args.steps // 2), H=H, D=D, bs=bs)
+        # a ragged length whose staged pack takes single-owner tiles
+        result["pack_ragged_single_owner"] = pack_ragged_leg(
+            dev, max(3, args.steps // 2), T=24001, H=H, D=D, bs=bs)
 
     if not args.no_dequant:
         result["dequant"] = dequant_leg(src_cache, T, bs, torch.zeros_like(dst_caches[0]),
@@ -416,10 +419,26 @@ def pack_ragged_leg(dev, steps, T=32753, layers=4, H=8, D=128, bs=16):
     src_tokens = caches[0].view(torch.uint8)[:, ids[0]].reshape(2, -1, H * C)[:, :T]
     ok = bool(torch.equal(outs[0].view(H * C, 2 * T), src_tokens.reshape(2 * T, H * C).t()))
     gbps = layers * layer_bytes / (ms * 1e-3) / 1e9
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
     return {"tokens": T, "layers": layers, "us_per_layer": round(1e3 * ms / layers, 2),
             "algorithmic_bytes_per_layer": layer_bytes, "gbps": round(gbps, 2),
             "frac": round(gbps / HBM_PEAK_GBPS, 4), "pack_ok": ok,
-            "kernel": "rows_pack_staged8_kernel<16, false> (8-bit runs off 128-byte lines)"}
+            "kernel": _staged_pack_kernel(T, H, C, cus)}
+
+
+def _staged_pack_kernel(T, H, C, cus):
+    """The staged pack kernel the library picks for T tokens of H heads x C
+    bytes on `cus` CUs (the host rule in set_pack_grid, restated for the
+    label): 16-wave tiles once they give half a tile per CU, single-owner
+    tiles of 1920 tokens when those take no more rounds of tiles per CU."""
+    cols = 2 * -(-H * C // 128)
+    tiles16 = cols * -(-T // 2048)
+    if tiles16 < max(1, cus // 2):
+        return "rows_pack_staged8_kernel (8- or 4-wave tiles; 8-bit runs off 128-byte lines)"
+    if -(-cols * -(-T // 1920) // cus) <= -(-tiles16 // cus):
+        return ("rows_pack_staged8_kernel<16, false, true> (single-owner tiles: each stream "
+                "line written by one tile)")
+    return "rows_pack_staged8_kernel<16, false> (8-bit runs off 128-byte lines)"
 
 
 def dequant_leg(src_cache, T, bs, dst_cache, dst_ids, gen, dev, steps, layers=4):
