@@ -125,10 +125,10 @@ def test_staged_pack_into_offset_stream(cuda_device, shift, T):
         "bytes outside the stream were written"
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(12))
 def test_staged_pack_random_geometries(cuda_device, seed):
     """Seeded staged packs at 5000-60000 odd token counts, 2-8 heads of 128
-    or 256 bytes, block size 16 or 32, both cache layouts and an output
+    or 256 bytes, block sizes 8, 16, 24 or 32, both cache layouts and an output
     pointer 0-64 bytes into its buffer.  Most of these draws take 16-wave
     tiles in which each stream line is written by one tile.  The stream
     equals the oracle's and the bytes around it keep their guard value."""
@@ -137,7 +137,7 @@ def test_staged_pack_random_geometries(cuda_device, seed):
     T = int(rng.integers(5000, 60000)) | 1
     H = int(rng.choice([2, 4, 8]))
     C = int(rng.choice([128, 256]))
-    bs = int(rng.choice([16, 32]))
+    bs = int(rng.choice([8, 16, 24, 32]))
     blocks_first = bool(rng.integers(0, 2))
     shift = int(rng.choice([0, 3, 64]))
     nblk = -(-T // bs)
