@@ -291,9 +291,10 @@ def main() -> int:
 
     if not args.no_pack_ragged:
         result["pack_ragged"] = pack_ragged_leg(dev, max(3, args.steps // 2), H=H, D=D, bs=bs)
-        # a ragged length whose staged pack takes single-owner tiles
+        # a ragged length whose staged pack takes single-owner tiles, in whole
+        # rounds of tiles per CU as pack_ragged's 32753 tokens are (2 rounds)
         result["pack_ragged_single_owner"] = pack_ragged_leg(
-            dev, max(3, args.steps // 2), T=24001, H=H, D=D, bs=bs)
+            dev, max(3, args.steps // 2), T=30001, H=H, D=D, bs=bs)
 
     if not args.no_dequant:
         result["dequant"] = dequant_leg(src_cache, T, bs, torch.zeros_like(dst_caches[0]),
